@@ -1,0 +1,133 @@
+/*
+ * nanoserve_paged.h -- C ABI of the MI355X (gfx950) paged-attention library.
+ *
+ * The library replaces the GPU side of nanoserve's attention op and KV-cache
+ * write.  Every entry point takes plain device pointers, element strides and
+ * sizes, and a HIP stream (passed as void*, e.g. the value of
+ * torch.cuda.current_stream().cuda_stream).  Nothing here allocates device
+ * memory, synchronises the device or keeps state between calls, except the
+ * split-K counters inside the caller-owned workspace (see
+ * ns_paged_attention_workspace_size).
+ *
+ * Layouts (unchanged from the reference):
+ *   query / out          [num_tokens, num_heads, head_dim], contiguous
+ *   k_cache / v_cache    [num_blocks, block_size, num_kv_heads, head_dim], contiguous
+ *   block_tables         [num_seqs, >= ceil(max_seq_len / block_size)], row stride given
+ *   seq_lens             [num_seqs]      context length including this step
+ *   query_start_loc      [num_seqs + 1]  prefix sums of the per-sequence query lengths
+ *   slot_mapping         [num_tokens]    slot = block_table[pos / bs] * bs + pos % bs
+ *
+ * Integer index tensors may be int32 or int64 (the engine ships int64, the
+ * reference tests int32); each pointer carries its own width flag so no cast
+ * kernel is ever needed.
+ *
+ * Every function returns NS_OK (0) or a negative NS_ERR_* code and never
+ * aborts the process.  Argument checks run on the host before any HIP call.
+ */
+#ifndef NANOSERVE_PAGED_H
+#define NANOSERVE_PAGED_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. */
+#define NS_OK 0
+#define NS_ERR_INVALID_ARG (-1)  /* null pointer, bad size, bad stride      */
+#define NS_ERR_UNSUPPORTED (-2)  /* shape/dtype combination not compiled   */
+#define NS_ERR_WORKSPACE (-3)    /* workspace missing or too small         */
+#define NS_ERR_HIP (-4)          /* the HIP launch itself reported an error */
+
+/* Element types. */
+#define NS_DTYPE_F32 0
+#define NS_DTYPE_F16 1
+#define NS_DTYPE_BF16 2
+
+/* Human-readable text for a status code (static storage, never NULL). */
+const char* ns_error_string(int code);
+
+/* Library version as MAJOR*10000 + MINOR*100 + PATCH. */
+int ns_version(void);
+
+/*
+ * ns_reshape_and_cache -- scatter this step's K and V rows into the paged cache.
+ *
+ * Replaces PagedKVCache.write (reference nanoserve/kv_cache.py:73-81):
+ *     k_cache.view(NB*BS, Hkv, D).index_copy_(0, slot_mapping, key.to(cache dtype))
+ *     v_cache.view(NB*BS, Hkv, D).index_copy_(0, slot_mapping, value.to(cache dtype))
+ * in one launch for both caches.  Same-dtype rows are copied bit for bit;
+ * f32 -> f16/bf16 and f16 <-> bf16 conversions round to nearest even like
+ * torch's Tensor.to (NaN becomes a canonical quiet NaN).  Slots outside
+ * [0, num_blocks*block_size) -- e.g. -1 for padding tokens -- are skipped and
+ * never dereferenced.
+ *
+ * key/value strides are in elements; the head_dim stride must be 1.
+ */
+int ns_reshape_and_cache(const void* key, const void* value,
+                         int64_t key_stride_token, int64_t key_stride_head,
+                         int64_t value_stride_token, int64_t value_stride_head,
+                         void* k_cache, void* v_cache,
+                         const void* slot_mapping, int slot_mapping_is_int64,
+                         int64_t num_tokens, int num_kv_heads, int head_dim,
+                         int block_size, int64_t num_blocks,
+                         int src_dtype, int cache_dtype, void* stream);
+
+/*
+ * ns_paged_attention_workspace_size -- bytes of device workspace that
+ * ns_paged_attention needs for these sizes (split-K partials and counters).
+ *
+ * The workspace must be zero-filled once when it is first allocated; every
+ * call leaves its counters at zero again, so the same buffer can be reused by
+ * later calls on the same stream without clearing.  Calls that overlap in
+ * time (different streams) must use different workspaces.
+ */
+size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
+                                         int head_dim, int block_size,
+                                         int max_seq_len, int max_query_len,
+                                         int64_t num_tokens, int is_decode_only);
+
+/*
+ * ns_paged_attention -- unified paged attention (prefill, decode, chunked
+ * prefill and mixed batches in one entry point).
+ *
+ * Replaces the attn_fn contract shared by paged_attention_torch
+ * (reference nanoserve/attention.py:99-151, decode fast path 154-190) and
+ * paged_attention_triton (reference nanoserve/triton_attention.py:117-161):
+ * query token j of sequence i sits at absolute position
+ * seq_lens[i] - query_len_i + j and attends to keys [0, that position] of
+ * that sequence, with kv head h / (num_heads / num_kv_heads), scores scaled
+ * by `scale`, softmax accumulated in fp32, output written in `dtype`.
+ *
+ * When is_decode_only is set every sequence has exactly one query token and
+ * token i belongs to sequence i (query_start_loc is not read), as in the
+ * reference decode fast path.  Otherwise query_start_loc delimits each
+ * sequence's query rows; sequences with an empty query range are skipped.
+ *
+ * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
+ * Supported: head_dim in {64, 128}; block_size a power of two in [8, 256];
+ * num_heads / num_kv_heads <= 16.  Loops are bounded by each sequence's
+ * length (never by the block-table width), so zero-padded table rows are
+ * safe.  A block id outside [0, num_blocks) is never dereferenced; the
+ * affected (sequence, head) outputs are written as NaN.
+ */
+int ns_paged_attention(void* out, const void* query,
+                       const void* k_cache, const void* v_cache,
+                       const void* block_tables, int64_t block_table_stride,
+                       int64_t block_table_width, int block_tables_is_int64,
+                       const void* seq_lens, int seq_lens_is_int64,
+                       const void* query_start_loc, int query_start_loc_is_int64,
+                       int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                       int is_decode_only,
+                       int num_heads, int num_kv_heads, int head_dim,
+                       int block_size, int64_t num_blocks,
+                       float scale, int dtype,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOSERVE_PAGED_H */

@@ -1,0 +1,179 @@
+"""Paged attention on MI355X: the attn_fn drop-in over the HIP kernels.
+
+`paged_attention_hip(query, k_cache, v_cache, md, scale)` keeps the signature
+and the semantics of the reference's unified op (nanoserve/attention.py:99-151,
+decode fast path 154-190, Triton wrapper triton_attention.py:117-161): prefill,
+decode, chunked prefill and mixed batches are one call; query row j of a
+sequence with context length L and query length ql attends to keys
+[0, L - ql + j]; the kv head of query head h is h // (Hq // Hkv).
+
+Everything runs on the GPU through libnanoserve_paged.so: a decode-only batch
+is one kernel launch (split-K partials are merged inside the launch), any
+other batch adds one launch of the variable-length MFMA kernel.  There is no
+torch or Triton fallback; a missing library or an unsupported shape raises.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+@dataclass
+class AttentionMetadata:
+    """Per-step addressing shared by all layers (reference attention.py:31-54).
+
+    Index tensors may be int32 or int64 and must live on the query's device.
+    The engine stages all of them as int64 slices of one buffer
+    (reference model_runner.py:128-137); the reference tests use int32.
+    """
+
+    slot_mapping: torch.Tensor      # [num_tokens] cache slot of each new token
+    query_start_loc: torch.Tensor   # [num_seqs + 1] prefix sums of query_lens
+    seq_lens: torch.Tensor          # [num_seqs] context length including this step
+    block_tables: torch.Tensor      # [num_seqs, max_blocks] physical block ids
+    max_query_len: int
+    max_seq_len: int
+    num_seqs: int
+    num_tokens: int
+    is_decode_only: bool            # every query_len == 1
+
+    query_lens_cpu: list[int] = None          # type: ignore[assignment]
+    seq_lens_cpu: list[int] = None            # type: ignore[assignment]
+    query_start_loc_cpu: list[int] = None     # type: ignore[assignment]
+
+
+_INDEX_DTYPES = (torch.int32, torch.int64)
+
+# Split-K workspaces, one per (device, stream).  The library requires the
+# buffer to be zero once and leaves its counters at zero after every call, so
+# a cached buffer is reused without clearing.  Calls on different streams may
+# overlap in time and therefore get different buffers.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        # Grow geometrically so a slowly growing max_seq_len reallocates rarely.
+        size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def _index(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype not in _INDEX_DTYPES:
+        t = t.to(torch.int64)
+    return t
+
+
+def workspace_bytes(md: AttentionMetadata, num_heads: int, num_kv_heads: int,
+                    head_dim: int, block_size: int) -> int:
+    """Device workspace ns_paged_attention needs for this metadata."""
+    return int(_lib.load().ns_paged_attention_workspace_size(
+        md.num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+        md.max_seq_len, md.max_query_len, md.num_tokens, int(bool(md.is_decode_only))))
+
+
+@torch.inference_mode()
+def paged_attention_hip(
+    query: torch.Tensor,        # [num_tokens, num_heads, head_dim]
+    k_cache: torch.Tensor,      # [num_blocks, block_size, num_kv_heads, head_dim]
+    v_cache: torch.Tensor,
+    md: AttentionMetadata,
+    scale: float,
+) -> torch.Tensor:
+    """Unified paged attention on the GPU.  Returns [num_tokens, num_heads, head_dim]."""
+    lib = _lib.load()
+    if query.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
+        raise ValueError(
+            f"expected query [T,Hq,D] and caches [NB,BS,Hkv,D], got "
+            f"{tuple(query.shape)}, {tuple(k_cache.shape)}, {tuple(v_cache.shape)}")
+    num_tokens, num_heads, head_dim = query.shape
+    num_blocks, block_size, num_kv_heads, cache_dim = k_cache.shape
+    if cache_dim != head_dim:
+        raise ValueError(f"head_dim mismatch: query {head_dim}, cache {cache_dim}")
+    if not query.is_cuda:
+        raise ValueError("paged_attention_hip needs GPU tensors (the HIP path has no CPU fallback)")
+    device = query.device
+    if k_cache.device != device or v_cache.device != device:
+        raise ValueError("query and caches must be on the same device")
+    if query.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise TypeError(f"query/cache dtypes differ: {query.dtype}, {k_cache.dtype}, {v_cache.dtype}")
+    if query.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"paged_attention_hip supports float16/bfloat16, got {query.dtype}")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous [num_blocks, block_size, num_kv_heads, head_dim]")
+    if md.num_tokens != num_tokens:
+        raise ValueError(f"metadata has {md.num_tokens} tokens, query has {num_tokens}")
+
+    q = query.contiguous()
+    out = torch.empty_like(q)
+    if num_tokens == 0 or md.num_seqs == 0:
+        return out.view(query.shape)
+
+    bt = _index(md.block_tables, "block_tables", device)
+    if bt.dim() != 2 or bt.shape[0] < md.num_seqs:
+        raise ValueError(f"block_tables must be [num_seqs, max_blocks], got {tuple(bt.shape)}")
+    if bt.stride(1) != 1:
+        bt = bt.contiguous()
+    max_blk = (md.max_seq_len + block_size - 1) // block_size
+    if bt.shape[1] < max_blk:
+        raise ValueError(
+            f"block_tables has {bt.shape[1]} columns but max_seq_len={md.max_seq_len} needs {max_blk}")
+    sl = _index(md.seq_lens, "seq_lens", device).contiguous()
+    decode_only = bool(md.is_decode_only)
+    if decode_only:
+        qsl_ptr, qsl64 = None, 0
+        if num_tokens != md.num_seqs:
+            raise ValueError("is_decode_only needs one query token per sequence")
+    else:
+        qsl = _index(md.query_start_loc, "query_start_loc", device).contiguous()
+        qsl_ptr, qsl64 = qsl.data_ptr(), int(qsl.dtype == torch.int64)
+
+    stream = torch.cuda.current_stream(device).cuda_stream
+    nbytes = lib.ns_paged_attention_workspace_size(
+        md.num_seqs, num_heads, num_kv_heads, head_dim, block_size,
+        md.max_seq_len, md.max_query_len, num_tokens, int(decode_only))
+    if nbytes == 0:
+        raise RuntimeError(
+            f"unsupported attention shape: Hq={num_heads} Hkv={num_kv_heads} D={head_dim} "
+            f"block_size={block_size}")
+    ws = _workspace(device, stream, nbytes)
+
+    rc = lib.ns_paged_attention(
+        out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        bt.data_ptr(), bt.stride(0), bt.shape[1], int(bt.dtype == torch.int64),
+        sl.data_ptr(), int(sl.dtype == torch.int64),
+        qsl_ptr, qsl64,
+        md.num_seqs, num_tokens, md.max_query_len, md.max_seq_len, int(decode_only),
+        num_heads, num_kv_heads, head_dim, block_size, num_blocks,
+        float(scale), _lib.DTYPE_CODES[q.dtype],
+        ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "ns_paged_attention")
+    return out.view(query.shape)
+
+
+def get_attention_backend(name: str = "auto"):
+    """Resolve a backend name to (callable, name) with attn_fn's signature.
+
+    Mirrors reference attention.py:193-206, with one backend: "auto" and "hip"
+    return the HIP path and raise if its library cannot be loaded.  The
+    reference's "torch" (gather+SDPA) and "triton" backends are not product
+    paths here and are rejected rather than silently substituted.
+    """
+    if name in ("auto", "hip"):
+        _lib.load()
+        return paged_attention_hip, "hip"
+    if name in ("torch", "triton"):
+        raise ValueError(
+            f"attention backend {name!r} is not provided: nanoserve_amd runs paged attention "
+            "only through its HIP kernels")
+    raise ValueError(f"unknown attention backend {name!r}")

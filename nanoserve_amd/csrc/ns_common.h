@@ -1,0 +1,88 @@
+// Shared device helpers for the gfx950 paged-attention kernels.
+//
+// Everything here is written for CDNA4 wave64: 16-byte per-lane global loads,
+// the 16x16x32 f16/bf16 MFMA, and cross-lane reductions inside a wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nanoserve_paged.h"
+
+namespace ns {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Element-type tags.  `vec8` is the 16-byte MFMA operand of eight elements,
+// `vec4` an 8-byte group of four.
+struct F16 {
+  using T = _Float16;
+  using vec8 = half8;
+  using vec4 = half4;
+  static constexpr int code = NS_DTYPE_F16;
+};
+struct BF16 {
+  using T = __bf16;
+  using vec8 = bf16x8;
+  using vec4 = bf16x4;
+  static constexpr int code = NS_DTYPE_BF16;
+};
+
+// D[16x16] += A[16x32] * B[32x16], fp32 accumulate.
+// Operand layout (lane l, group g = l / 16): A row l % 16 and B column l % 16,
+// each holding the 8 k-slots of group g.  The result layout is
+// D[4 * g + r][l % 16] in element r of the returned vector.
+__device__ __forceinline__ floatx4 mfma16x16x32(F16, half8 a, half8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16x16x32(BF16, bf16x8 a, bf16x8 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+template <class DT>
+__device__ __forceinline__ typename DT::vec8 load16(const void* p) {
+  return __builtin_bit_cast(typename DT::vec8, *reinterpret_cast<const u32x4*>(p));
+}
+
+template <class DT>
+__device__ __forceinline__ typename DT::vec8 zero8() {
+  return __builtin_bit_cast(typename DT::vec8, u32x4{0u, 0u, 0u, 0u});
+}
+
+// Load entry i of an int32 or int64 index tensor.
+__device__ __forceinline__ int64_t load_index(const void* p, int64_t i, int is64) {
+  return is64 ? reinterpret_cast<const int64_t*>(p)[i]
+              : static_cast<int64_t>(reinterpret_cast<const int32_t*>(p)[i]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Butterfly max / sum over the four 16-lane groups of a wave (lanes l, l^16,
+// l^32, l^48 hold the same matrix column in the MFMA result layout).
+__device__ __forceinline__ float group4_max(float v) {
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float group4_sum(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// LDS ordering between lanes of one wave: LDS instructions of a wave execute
+// in order, so a compiler-level fence is enough to make one lane's ds_write
+// visible to another lane's later ds_read.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace ns

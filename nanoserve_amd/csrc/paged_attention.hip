@@ -1,0 +1,651 @@
+// Paged attention for gfx950 (MI355X): decode with in-launch split-K merge,
+// and a variable-length (prefill / chunked prefill / mixed) kernel.
+//
+// Semantics follow the reference's unified op (nanoserve/attention.py:99-190):
+// query row j of a sequence with context length L and query length ql sits at
+// absolute position L - ql + j and attends to keys [0, L - ql + j]; kv head of
+// query head h is h / (Hq / Hkv); scores are scaled by `scale`; the softmax is
+// accumulated in fp32; the output is written in the query dtype.
+//
+// Both kernels compute S^T = K * Q^T with v_mfma_f32_16x16x32_{f16,bf16}:
+// the 16 MFMA rows are KV tokens and the 16 MFMA columns are query heads of
+// one GQA group (decode) or flattened (query row, head) pairs (prefill).  With
+// K as the A operand, a lane's 8 k-slots are 8 consecutive head dims of one
+// token, i.e. one 16-byte load straight out of the [NB, BS, Hkv, D] cache.
+// The result puts tokens 4*g + r (g = lane / 16) of column lane % 16 in lane
+// registers, which is exactly the B operand P^T of the O^T = V^T * P^T MFMA
+// once the k-slots of two 16-token tiles are interleaved, so P never moves
+// between lanes.  V^T is staged through LDS.
+#include <math.h>
+
+#include "ns_common.h"
+
+namespace ns {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * 64;
+
+struct AttnParams {
+  char* out;
+  const char* query;
+  const char* k_cache;
+  const char* v_cache;
+  const void* bt;
+  int64_t bt_stride;
+  const void* seq_lens;
+  const void* qsl;
+  int bt64, sl64, qsl64;
+  int decode_only;
+  int64_t num_tokens;     // rows of query/out; query rows outside are never touched
+  int num_heads, num_kv_heads, group;
+  int bs_shift;
+  int64_t num_blocks;
+  int64_t max_ctx;        // tokens addressable through a table row
+  float scale_log2;       // scale * log2(e): softmax runs in base 2
+  int split_tokens;       // decode: context tokens per workgroup
+  int max_splits;         // decode: workgroups per (sequence, kv head)
+  int skip_decode_rows;   // varlen: one-row sequences belong to the decode kernel
+  float* part_o;          // [S, Hkv, max_splits, G, D]  unnormalised partial outputs
+  float* part_ml;         // [S, Hkv, max_splits, G, 2]  (running max, running sum)
+  unsigned* counters;     // [S, Hkv] arrivals per (sequence, kv head); left at zero
+};
+
+// --------------------------------------------------------------------------
+// Decode: one workgroup per (sequence, kv head, context split).
+// --------------------------------------------------------------------------
+template <int D>
+struct DecodeCfg {
+  static constexpr int CH = D == 64 ? 64 : 32;  // tokens per wave per step (8 KiB of K+V)
+  static constexpr int NT = CH / 16;            // 16-token MFMA tiles per step
+  static constexpr int NC = D / 32;             // k-chunks of the QK^T contraction
+  static constexpr int NN = D / 16;             // 16-dim tiles of the output
+  static constexpr int VT_LD = CH + 4;          // padded row of the transposed V tile
+  static constexpr int LDS_V = kWaves * D * VT_LD * 2;
+  static constexpr int LDS_RED = (kWaves * 16 * D + 2 * kWaves * 16) * 4;
+  static constexpr int LDS = LDS_V > LDS_RED ? LDS_V : LDS_RED;
+  static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
+};
+
+template <class DT, int D>
+__global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
+  using Cfg = DecodeCfg<D>;
+  using T = typename DT::T;
+  using V8 = typename DT::vec8;
+  constexpr int CH = Cfg::CH, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, VT_LD = Cfg::VT_LD;
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
+  __shared__ int s_last;
+
+  const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int G = p.group, Hkv = p.num_kv_heads;
+
+  int64_t qtok = s;
+  if (!p.decode_only) {
+    const int64_t q0 = load_index(p.qsl, s, p.qsl64);
+    const int64_t q1 = load_index(p.qsl, s + 1, p.qsl64);
+    if (q1 - q0 != 1) return;  // not a decode row: the varlen kernel owns it
+    qtok = q0;
+  }
+  if (qtok < 0 || qtok >= p.num_tokens) return;
+  int64_t L = load_index(p.seq_lens, s, p.sl64);
+  L = L < p.max_ctx ? L : p.max_ctx;
+  T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
+  const int64_t t_split0 = static_cast<int64_t>(split) * p.split_tokens;
+  if (t_split0 >= L) {
+    // No key is visible: the reference's masked softmax yields zeros.
+    if (split == 0)
+      for (int i = tid; i < G * D; i += kThreads) out_row[i] = static_cast<T>(0.f);
+    return;
+  }
+  const int64_t t_split1 = L < t_split0 + p.split_tokens ? L : t_split0 + p.split_tokens;
+  const int nsplit = static_cast<int>((L + p.split_tokens - 1) / p.split_tokens);
+  const int bs_mask = (1 << p.bs_shift) - 1;
+
+  // Q^T operand: column c16 is query head kvh*G + c16 (zero past the group).
+  V8 qop[NC];
+  {
+    const T* qrow = reinterpret_cast<const T*>(p.query) +
+                    (qtok * p.num_heads + static_cast<int64_t>(kvh) * G + c16) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qop[c] = c16 < G ? load16<DT>(qrow + 32 * c + 8 * g) : zero8<DT>();
+  }
+
+  T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
+  float m_run = -INFINITY, l_run = 0.f;
+  floatx4 acc[NN];
+#pragma unroll
+  for (int n = 0; n < NN; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  int bad = 0;
+  const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between slots
+  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
+  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
+  const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
+
+  for (int64_t tb = t_split0 + w * CH; tb < t_split1; tb += kWaves * CH) {
+    V8 kr[NT][NC], vr[NT][NC];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t t = tb + 16 * j + c16;
+      bool valid = t < t_split1;
+      int64_t blk = 0;
+      if (valid) blk = load_index(p.bt, bt_row + (t >> p.bs_shift), p.bt64);
+      if (valid && (blk < 0 || blk >= p.num_blocks)) {
+        bad = 1;
+        valid = false;
+      }
+      if (!valid) blk = 0;  // addresses are formed from in-range blocks only
+      const int64_t off = ((blk << p.bs_shift) + (t & bs_mask)) * slot_stride;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        kr[j][c] = valid ? load16<DT>(kbase + off + 32 * c) : zero8<DT>();
+        vr[j][c] = valid ? load16<DT>(vbase + off + 32 * c) : zero8<DT>();
+      }
+    }
+    // Stage V transposed (vt[dim][token]) for the PV operand.
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(32 * c + 8 * g + e) * VT_LD + 16 * j + c16] = vr[j][c][e];
+
+    // S^T = K Q^T: sacc[j][r] = score of token tb + 16j + 4g + r, head c16.
+    floatx4 sacc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      sacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) sacc[j] = mfma16x16x32(DT{}, kr[j][c], qop[c], sacc[j]);
+    }
+    float sv[NT][4];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t t = tb + 16 * j + 4 * g + r;
+        const float x = t < t_split1 ? sacc[j][r] * p.scale_log2 : -INFINITY;
+        sv[j][r] = x;
+        mloc = fmaxf(mloc, x);
+      }
+    mloc = group4_max(mloc);
+    const float m_new = fmaxf(m_run, mloc);
+    const bool none = m_new == -INFINITY;
+    const float alpha = none ? 1.f : fast_exp2(m_run - m_new);
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float pr = none ? 0.f : fast_exp2(sv[j][r] - m_new);
+        sv[j][r] = pr;
+        psum += pr;
+      }
+    l_run = l_run * alpha + psum;
+#pragma unroll
+    for (int n = 0; n < NN; ++n) acc[n] *= alpha;
+    m_run = m_new;
+
+    wave_lds_sync();
+    // O^T += V^T P^T over 32-token pairs: k-slot e of group g is token 4g+e of
+    // the even tile (e < 4) or of the odd tile (e >= 4).
+#pragma unroll
+    for (int pb = 0; pb < NT / 2; ++pb) {
+      V8 pt;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pt[e] = static_cast<T>(sv[2 * pb][e]);
+        pt[4 + e] = static_cast<T>(sv[2 * pb + 1][e]);
+      }
+#pragma unroll
+      for (int n = 0; n < NN; ++n) {
+        const T* r0 = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
+        const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        acc[n] = mfma16x16x32(DT{}, va, pt, acc[n]);
+      }
+    }
+    wave_lds_sync();
+  }
+  l_run = group4_sum(l_run);
+
+  // Merge the four waves' (max, sum, O) through LDS.
+  bad = __syncthreads_or(bad);
+  float* red_o = reinterpret_cast<float*>(smem);
+  float* red_m = red_o + kWaves * 16 * D;
+  float* red_l = red_m + kWaves * 16;
+#pragma unroll
+  for (int n = 0; n < NN; ++n)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red_o[(w * 16 + c16) * D + 16 * n + 4 * g + r] = acc[n][r];
+  if (g == 0) {
+    red_m[w * 16 + c16] = m_run;
+    red_l[w * 16 + c16] = l_run;
+  }
+  __syncthreads();
+
+  const int nout = G * D;
+  const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
+  for (int i = tid; i < nout; i += kThreads) {
+    const int col = i / D, d = i - col * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red_m[ww * 16 + col]);
+    float lsum = 0.f, o = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float mw = red_m[ww * 16 + col];
+      if (mw != -INFINITY) {
+        const float sc = fast_exp2(mw - M);
+        lsum += red_l[ww * 16 + col] * sc;
+        o += red_o[(ww * 16 + col) * D + d] * sc;
+      }
+    }
+    if (bad) lsum = o = NAN;
+    if (nsplit == 1) {
+      out_row[i] = static_cast<T>(lsum > 0.f || lsum != lsum ? o / lsum : 0.f);
+    } else {
+      const int64_t pi = (pair * p.max_splits + split) * G + col;
+      p.part_o[pi * D + d] = o;
+      if (d == 0) {
+        p.part_ml[pi * 2] = M;
+        p.part_ml[pi * 2 + 1] = lsum;
+      }
+    }
+  }
+  if (nsplit == 1) return;
+
+  // Split-K merge inside the same launch: the last workgroup of this
+  // (sequence, kv head) to arrive combines every split's partial.
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prev = atomicAdd(&p.counters[pair], 1u);
+    s_last = prev == static_cast<unsigned>(nsplit - 1);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+  for (int i = tid; i < nout; i += kThreads) {
+    const int col = i / D, d = i - col * D;
+    const int64_t p0 = pair * p.max_splits * G + col;
+    float M = -INFINITY;
+    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, p.part_ml[(p0 + sp * G) * 2]);
+    float lsum = 0.f, o = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const int64_t pi = p0 + sp * G;
+      const float sc = fast_exp2(p.part_ml[pi * 2] - M);
+      lsum += p.part_ml[pi * 2 + 1] * sc;
+      o += p.part_o[pi * D + d] * sc;
+    }
+    out_row[i] = static_cast<T>(lsum > 0.f || lsum != lsum ? o / lsum : 0.f);
+  }
+  if (tid == 0) __hip_atomic_store(&p.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// --------------------------------------------------------------------------
+// Variable-length rows (prefill, chunked prefill, the prefill part of a mixed
+// batch): one workgroup per (sequence, kv head, block of 128 flattened
+// (query row, head) columns); K and V stream through LDS in 32-token stages
+// shared by the four waves.
+// --------------------------------------------------------------------------
+template <int D>
+struct VarlenCfg {
+  static constexpr int KC = 32;                  // KV tokens per LDS stage
+  static constexpr int CT = 2;                   // 16-column tiles per wave
+  static constexpr int COLS = kWaves * CT * 16;  // columns per workgroup
+  static constexpr int NC = D / 32, NN = D / 16;
+  static constexpr int K_LD = D + 8;             // padded K row (elements)
+  static constexpr int VT_LD = KC + 4;           // padded V^T row (elements)
+  static constexpr int CHUNKS = KC * D / 8;      // 16-byte chunks per stage per tensor
+  static constexpr int CPT = CHUNKS / kThreads;  // per thread
+  static_assert(CHUNKS % kThreads == 0, "stage must split evenly over the workgroup");
+};
+
+template <class DT, int D>
+__global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
+  using Cfg = VarlenCfg<D>;
+  using T = typename DT::T;
+  using V8 = typename DT::vec8;
+  constexpr int KC = Cfg::KC, CT = Cfg::CT, COLS = Cfg::COLS, NC = Cfg::NC, NN = Cfg::NN;
+  constexpr int K_LD = Cfg::K_LD, VT_LD = Cfg::VT_LD, CPT = Cfg::CPT;
+  __shared__ __attribute__((aligned(16))) T k_lds[KC * K_LD];
+  __shared__ __attribute__((aligned(16))) T vt_lds[D * VT_LD];
+
+  const int cb = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int G = p.group, Hkv = p.num_kv_heads;
+
+  const int64_t q0 = load_index(p.qsl, s, p.qsl64);
+  const int64_t ql = load_index(p.qsl, s + 1, p.qsl64) - q0;
+  if (ql <= 0 || (p.skip_decode_rows && ql == 1)) return;
+  if (q0 < 0 || q0 + ql > p.num_tokens) return;
+  const int64_t ncols = ql * G;
+  const int64_t c_begin = static_cast<int64_t>(cb) * COLS;
+  if (c_begin >= ncols) return;
+  int64_t L = load_index(p.seq_lens, s, p.sl64);
+  L = L < p.max_ctx ? L : p.max_ctx;
+  const int64_t ctx0 = L - ql;  // absolute position of query row 0
+  const int bs_mask = (1 << p.bs_shift) - 1;
+
+  V8 qop[CT][NC];
+  int64_t qpos[CT], orow[CT];
+  bool cval[CT];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const int64_t c = c_begin + (w * CT + ct) * 16 + c16;
+    cval[ct] = c < ncols;
+    const int64_t qi = cval[ct] ? c / G : 0;
+    const int64_t h = cval[ct] ? c - qi * G : 0;
+    qpos[ct] = ctx0 + qi;
+    orow[ct] = ((q0 + qi) * p.num_heads + static_cast<int64_t>(kvh) * G + h) * D;
+    const T* qrow = reinterpret_cast<const T*>(p.query) + orow[ct];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+      qop[ct][c] = cval[ct] ? load16<DT>(qrow + 32 * c + 8 * g) : zero8<DT>();
+  }
+  const int64_t c_last = (ncols < c_begin + COLS ? ncols : c_begin + COLS) - 1;
+  int64_t kv_end = ctx0 + c_last / G + 1;
+  kv_end = kv_end < L ? kv_end : L;
+
+  float m_run[CT], l_run[CT];
+  floatx4 acc[CT][NN];
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    m_run[ct] = -INFINITY;
+    l_run[ct] = 0.f;
+#pragma unroll
+    for (int n = 0; n < NN; ++n) acc[ct][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  int bad = 0;
+  const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;
+  const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
+
+  for (int64_t t0 = 0; t0 < kv_end; t0 += KC) {
+    u32x4 kraw[CPT], vraw[CPT];
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int idx = tid + i * kThreads;
+      const int tok = idx / (D / 8), ch = idx % (D / 8);
+      const int64_t t = t0 + tok;
+      bool valid = t < kv_end;
+      int64_t blk = 0;
+      if (valid) blk = load_index(p.bt, bt_row + (t >> p.bs_shift), p.bt64);
+      if (valid && (blk < 0 || blk >= p.num_blocks)) {
+        bad = 1;
+        valid = false;
+      }
+      if (!valid) blk = 0;
+      const int64_t off = ((blk << p.bs_shift) + (t & bs_mask)) * slot_stride + static_cast<int64_t>(kvh) * D + ch * 8;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      kraw[i] = valid ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(p.k_cache) + off) : z;
+      vraw[i] = valid ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(p.v_cache) + off) : z;
+    }
+    __syncthreads();  // previous stage fully consumed
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int idx = tid + i * kThreads;
+      const int tok = idx / (D / 8), ch = idx % (D / 8);
+      *reinterpret_cast<u32x4*>(k_lds + tok * K_LD + ch * 8) = kraw[i];
+      const V8 v8 = __builtin_bit_cast(V8, vraw[i]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) vt_lds[(ch * 8 + e) * VT_LD + tok] = v8[e];
+    }
+    __syncthreads();
+
+    V8 ka[2][NC];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int c = 0; c < NC; ++c)
+        ka[j][c] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(k_lds + (16 * j + c16) * K_LD + 32 * c + 8 * g));
+    V8 pt[CT];
+#pragma unroll
+    for (int ct = 0; ct < CT; ++ct) {
+      floatx4 sacc[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        sacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; ++c) sacc[j] = mfma16x16x32(DT{}, ka[j][c], qop[ct][c], sacc[j]);
+      }
+      float sv[2][4];
+      float mloc = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t t = t0 + 16 * j + 4 * g + r;
+          const bool ok = cval[ct] && t <= qpos[ct] && t < L;
+          const float x = ok ? sacc[j][r] * p.scale_log2 : -INFINITY;
+          sv[j][r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+      mloc = group4_max(mloc);
+      const float m_new = fmaxf(m_run[ct], mloc);
+      const bool none = m_new == -INFINITY;
+      const float alpha = none ? 1.f : fast_exp2(m_run[ct] - m_new);
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float pr = none ? 0.f : fast_exp2(sv[j][r] - m_new);
+          sv[j][r] = pr;
+          psum += pr;
+        }
+      l_run[ct] = l_run[ct] * alpha + psum;
+#pragma unroll
+      for (int n = 0; n < NN; ++n) acc[ct][n] *= alpha;
+      m_run[ct] = m_new;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        pt[ct][e] = static_cast<T>(sv[0][e]);
+        pt[ct][4 + e] = static_cast<T>(sv[1][e]);
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < NN; ++n) {
+      const T* r0 = vt_lds + (16 * n + c16) * VT_LD + 4 * g;
+      const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
+      const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
+      const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) acc[ct][n] = mfma16x16x32(DT{}, va, pt[ct], acc[ct][n]);
+    }
+  }
+  bad = __syncthreads_or(bad);
+
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) {
+    const float lsum = group4_sum(l_run[ct]);
+    if (!cval[ct]) continue;
+    const float inv = bad ? NAN : (lsum > 0.f ? 1.f / lsum : 0.f);
+    T* orow_p = reinterpret_cast<T*>(p.out) + orow[ct];
+#pragma unroll
+    for (int n = 0; n < NN; ++n) {
+      typename DT::vec4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(acc[ct][n][r] * inv);
+      *reinterpret_cast<u32x2*>(orow_p + 16 * n + 4 * g) = __builtin_bit_cast(u32x2, v4);
+    }
+  }
+}
+
+// --------------------------------------------------------------------------
+// Host side.
+// --------------------------------------------------------------------------
+struct DecodePlan {
+  int split_tokens;
+  int max_splits;
+};
+
+// Tokens per decode workgroup: the four waves' first step, doubled until a
+// sequence needs at most 64 workgroups, which bounds the partial buffers
+// while giving short batches enough workgroups to cover 256 CUs.
+DecodePlan plan_decode(int head_dim, int64_t ctx_tokens) {
+  const int base = kWaves * (head_dim == 64 ? DecodeCfg<64>::CH : DecodeCfg<128>::CH);
+  int64_t tok = base;
+  while ((ctx_tokens + tok - 1) / tok > 64) tok *= 2;
+  DecodePlan plan;
+  plan.split_tokens = static_cast<int>(tok);
+  plan.max_splits = static_cast<int>(ctx_tokens <= 0 ? 1 : (ctx_tokens + tok - 1) / tok);
+  return plan;
+}
+
+struct WorkspaceLayout {
+  size_t counters_off, ml_off, o_off, total;
+};
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+WorkspaceLayout workspace_layout(int num_seqs, int num_kv_heads, int group, int head_dim,
+                                 const DecodePlan& plan) {
+  const size_t pairs = static_cast<size_t>(num_seqs) * num_kv_heads;
+  const size_t parts = pairs * plan.max_splits * group;
+  WorkspaceLayout l;
+  l.counters_off = 0;
+  l.ml_off = align_up(pairs * sizeof(unsigned), 256);
+  l.o_off = align_up(l.ml_off + parts * 2 * sizeof(float), 256);
+  l.total = align_up(l.o_off + parts * head_dim * sizeof(float), 256);
+  return l;
+}
+
+int ilog2_exact(int v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+int64_t round_up_ctx(int max_seq_len, int block_size) {
+  return (static_cast<int64_t>(max_seq_len) + block_size - 1) / block_size * block_size;
+}
+
+template <class DT, int D>
+hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipStream_t stream) {
+  void* args[] = {&p};
+  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&paged_decode_kernel<DT, D>),
+                                 dim3(p.max_splits, p.num_kv_heads, num_seqs), dim3(kThreads),
+                                 args, 0, stream);
+  if (e != hipSuccess || p.decode_only) return e;
+  const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
+  const int64_t nblk = (cols + VarlenCfg<D>::COLS - 1) / VarlenCfg<D>::COLS;
+  if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
+  return hipLaunchKernel(reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D>),
+                         dim3(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs),
+                         dim3(kThreads), args, 0, stream);
+}
+
+bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
+
+}  // namespace
+}  // namespace ns
+
+extern "C" const char* ns_error_string(int code) {
+  switch (code) {
+    case NS_OK: return "ok";
+    case NS_ERR_INVALID_ARG: return "invalid argument";
+    case NS_ERR_UNSUPPORTED: return "unsupported shape or dtype";
+    case NS_ERR_WORKSPACE: return "workspace missing or too small";
+    case NS_ERR_HIP: return "HIP launch failed";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int ns_version(void) { return 100; }
+
+extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
+                                                    int head_dim, int block_size,
+                                                    int max_seq_len, int max_query_len,
+                                                    int64_t num_tokens, int is_decode_only) {
+  (void)max_query_len;
+  (void)num_tokens;
+  (void)is_decode_only;
+  if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads ||
+      block_size <= 0 || max_seq_len < 0 || (head_dim != 64 && head_dim != 128))
+    return 0;
+  const ns::DecodePlan plan = ns::plan_decode(head_dim, ns::round_up_ctx(max_seq_len, block_size));
+  return ns::workspace_layout(num_seqs, num_kv_heads, num_heads / num_kv_heads, head_dim, plan).total;
+}
+
+extern "C" int ns_paged_attention(void* out, const void* query,
+                                  const void* k_cache, const void* v_cache,
+                                  const void* block_tables, int64_t block_table_stride,
+                                  int64_t block_table_width, int block_tables_is_int64,
+                                  const void* seq_lens, int seq_lens_is_int64,
+                                  const void* query_start_loc, int query_start_loc_is_int64,
+                                  int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                                  int is_decode_only,
+                                  int num_heads, int num_kv_heads, int head_dim,
+                                  int block_size, int64_t num_blocks,
+                                  float scale, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace ns;
+  if (num_seqs < 0 || num_tokens < 0) return NS_ERR_INVALID_ARG;
+  if (num_seqs == 0 || num_tokens == 0) return NS_OK;
+  if (!out || !query || !k_cache || !v_cache || !block_tables || !seq_lens) return NS_ERR_INVALID_ARG;
+  if (!is_decode_only && !query_start_loc) return NS_ERR_INVALID_ARG;
+  if (is_decode_only && num_tokens != num_seqs) return NS_ERR_INVALID_ARG;
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads) return NS_ERR_INVALID_ARG;
+  if (num_blocks <= 0 || block_table_width <= 0 || block_table_stride < block_table_width)
+    return NS_ERR_INVALID_ARG;
+  if (max_seq_len < 0 || max_query_len < 0) return NS_ERR_INVALID_ARG;
+  if (!(scale == scale)) return NS_ERR_INVALID_ARG;
+  const int bs_shift = ilog2_exact(block_size);
+  if (bs_shift < 0) return NS_ERR_UNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128) return NS_ERR_UNSUPPORTED;
+  if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
+  const int group = num_heads / num_kv_heads;
+  if (group > 16) return NS_ERR_UNSUPPORTED;
+  if (num_seqs > 65535 || num_kv_heads > 65535) return NS_ERR_UNSUPPORTED;
+  if (!aligned16(out) || !aligned16(query) || !aligned16(k_cache) || !aligned16(v_cache))
+    return NS_ERR_INVALID_ARG;
+
+  const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
+  const DecodePlan plan = plan_decode(head_dim, ctx_plan);
+  const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan);
+  if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
+
+  AttnParams p;
+  p.out = static_cast<char*>(out);
+  p.query = static_cast<const char*>(query);
+  p.k_cache = static_cast<const char*>(k_cache);
+  p.v_cache = static_cast<const char*>(v_cache);
+  p.bt = block_tables;
+  p.bt_stride = block_table_stride;
+  p.seq_lens = seq_lens;
+  p.qsl = query_start_loc;
+  p.bt64 = block_tables_is_int64 ? 1 : 0;
+  p.sl64 = seq_lens_is_int64 ? 1 : 0;
+  p.qsl64 = query_start_loc_is_int64 ? 1 : 0;
+  p.decode_only = is_decode_only ? 1 : 0;
+  p.num_tokens = num_tokens;
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.group = group;
+  p.bs_shift = bs_shift;
+  p.num_blocks = num_blocks;
+  const int64_t table_tokens = block_table_width * static_cast<int64_t>(block_size);
+  p.max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.split_tokens = plan.split_tokens;
+  p.max_splits = plan.max_splits;
+  p.skip_decode_rows = 1;
+  char* ws = static_cast<char*>(workspace);
+  p.counters = reinterpret_cast<unsigned*>(ws + wl.counters_off);
+  p.part_ml = reinterpret_cast<float*>(ws + wl.ml_off);
+  p.part_o = reinterpret_cast<float*>(ws + wl.o_off);
+
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (dtype == NS_DTYPE_F16)
+    e = head_dim == 64 ? launch_attention<F16, 64>(p, num_seqs, max_query_len, st)
+                       : launch_attention<F16, 128>(p, num_seqs, max_query_len, st);
+  else
+    e = head_dim == 64 ? launch_attention<BF16, 64>(p, num_seqs, max_query_len, st)
+                       : launch_attention<BF16, 128>(p, num_seqs, max_query_len, st);
+  return e == hipSuccess ? NS_OK : NS_ERR_HIP;
+}

@@ -1,0 +1,112 @@
+"""The C-ABI library: it loads, exports every declared symbol, and rejects bad
+arguments on the host before touching the GPU (runs without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanoserve_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "nanoserve_paged.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ns_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    for n in ("ns_reshape_and_cache", "ns_paged_attention", "ns_paged_attention_workspace_size",
+              "ns_error_string", "ns_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(_declared_functions()) == set(_lib.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    lib = _lib.load()
+    assert lib.ns_version() >= 100
+    for code in (0, -1, -2, -3, -4):
+        assert lib.ns_error_string(code)
+    assert lib.ns_error_string(-99) == b"unknown status"
+
+
+def _attn_args(**over):
+    a = dict(out=16, query=16, k_cache=16, v_cache=16, bt=16, bt_stride=4, bt_width=4, bt64=0,
+             sl=16, sl64=0, qsl=16, qsl64=0, S=2, T=2, maxq=1, maxs=64, decode_only=1,
+             Hq=14, Hkv=2, D=64, bs=16, nb=32, scale=0.125, dtype=_lib.NS_DTYPE_F16,
+             ws=16, ws_bytes=1 << 30, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(out=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(bt=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(decode_only=0, qsl=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(T=3), _lib.NS_ERR_INVALID_ARG),                 # decode-only needs T == S
+    (dict(Hq=15), _lib.NS_ERR_INVALID_ARG),               # Hq not a multiple of Hkv
+    (dict(D=96), _lib.NS_ERR_UNSUPPORTED),
+    (dict(bs=24), _lib.NS_ERR_UNSUPPORTED),               # not a power of two
+    (dict(dtype=_lib.NS_DTYPE_F32), _lib.NS_ERR_UNSUPPORTED),
+    (dict(Hq=64, Hkv=2), _lib.NS_ERR_UNSUPPORTED),        # 32 query heads per kv head
+    (dict(ws=None), _lib.NS_ERR_WORKSPACE),
+    (dict(ws_bytes=8), _lib.NS_ERR_WORKSPACE),
+    (dict(bt_stride=2), _lib.NS_ERR_INVALID_ARG),         # stride below width
+    (dict(out=18), _lib.NS_ERR_INVALID_ARG),              # misaligned output
+    (dict(scale=float("nan")), _lib.NS_ERR_INVALID_ARG),
+])
+def test_paged_attention_rejects_bad_arguments(over, code):
+    lib = _lib.load()
+    assert lib.ns_paged_attention(*_attn_args(**over)) == code
+
+
+def test_empty_batch_is_a_no_op():
+    lib = _lib.load()
+    assert lib.ns_paged_attention(*_attn_args(S=0, T=0, out=None)) == _lib.NS_OK
+
+
+def test_workspace_size_is_monotone_in_context():
+    lib = _lib.load()
+    sizes = [lib.ns_paged_attention_workspace_size(32, 14, 2, 64, 16, L, 1, 32, 1)
+             for L in (16, 256, 1024, 8192, 65536)]
+    assert all(s > 0 for s in sizes)
+    assert sizes == sorted(sizes)
+    assert lib.ns_paged_attention_workspace_size(32, 14, 2, 96, 16, 100, 1, 32, 1) == 0
+
+
+def _rc_args(**over):
+    a = dict(key=16, value=16, kst=128, ksh=64, vst=128, vsh=64, kc=16, vc=16, slots=16, s64=1,
+             T=4, Hkv=2, D=64, bs=16, nb=8, src=_lib.NS_DTYPE_F16, dst=_lib.NS_DTYPE_F16, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(key=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(slots=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(Hkv=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(src=7), _lib.NS_ERR_UNSUPPORTED),
+    (dict(D=60), _lib.NS_ERR_UNSUPPORTED),                # rows not a whole number of 16-byte chunks
+    (dict(kc=18), _lib.NS_ERR_INVALID_ARG),
+])
+def test_reshape_and_cache_rejects_bad_arguments(over, code):
+    lib = _lib.load()
+    assert lib.ns_reshape_and_cache(*_rc_args(**over)) == code
+
+
+def test_reshape_and_cache_zero_tokens_is_a_no_op():
+    lib = _lib.load()
+    assert lib.ns_reshape_and_cache(*_rc_args(T=0, key=None)) == _lib.NS_OK
