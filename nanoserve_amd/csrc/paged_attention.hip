@@ -52,34 +52,141 @@ struct AttnParams {
 };
 
 // --------------------------------------------------------------------------
-// Decode: one workgroup per (sequence, kv head, context split).
+// Decode: one workgroup of W waves per (sequence, kv head, context split).
 // --------------------------------------------------------------------------
-template <int D>
+template <int D, int W, int CH_>
 struct DecodeCfg {
-  static constexpr int CH = D == 64 ? 64 : 32;  // tokens per wave per step (8 KiB of K+V)
+  static constexpr int kThreads = W * 64;
+  static constexpr int CH = CH_;                // tokens per wave per step
   static constexpr int NT = CH / 16;            // 16-token MFMA tiles per step
   static constexpr int NC = D / 32;             // k-chunks of the QK^T contraction
   static constexpr int NN = D / 16;             // 16-dim tiles of the output
   static constexpr int VT_LD = CH + 4;          // padded row of the transposed V tile
-  static constexpr int LDS_V = kWaves * D * VT_LD * 2;
-  static constexpr int LDS_RED = (kWaves * 16 * D + 2 * kWaves * 16) * 4;
+  static constexpr int LDS_V = W * D * VT_LD * 2;
+  static constexpr int LDS_RED = (W * 16 * D + 2 * W * 16) * 4;
   static constexpr int LDS = LDS_V > LDS_RED ? LDS_V : LDS_RED;
   static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
 };
 
-template <class DT, int D>
-__global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
-  using Cfg = DecodeCfg<D>;
+// Partial results of split sp of pair (sequence, kv head) live in the
+// workspace as part_ml[2 * ((pair * max_splits + sp) * G + col) + {0, 1}] =
+// (running max, running sum) and part_o[((pair * max_splits + sp) * G + col) * D + d].
+//
+// They cross workgroups (and XCDs, whose L2s are not coherent with each
+// other) through device-scope atomic accesses: the stores write through to
+// the device coherence point and the loads bypass the non-coherent caches, so
+// ordering the stores before the arrival counter (s_waitcnt) is all the
+// synchronisation the merge needs; no L2 writeback or invalidate is issued.
+__device__ __forceinline__ float part_load(const float* q) {
+  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void part_store(float* q, float v) {
+  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ void merge_into(float& m, float& l, floatx4& o, float m2, float l2, floatx4 o2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;  // both empty
+  const float a = fast_exp2(m - mn), b = fast_exp2(m2 - mn);
+  l = l * a + l2 * b;
+  o = o * a + o2 * b;
+  m = mn;
+}
+
+// Combine the nsplit partials of one pair into out_row ([G, D] of this kv
+// head's query heads).  All THREADS threads take part; each float4 column
+// (head, 4 dims) is owned by tpi consecutive lanes that walk disjoint split
+// subsets with up to 8 loads in flight, then merge by butterfly, so the
+// result does not depend on timing.
+template <class DT, int D, int THREADS>
+__device__ void merge_splits(const AttnParams& p, int64_t pair, int nsplit, typename DT::T* out_row) {
+  using T = typename DT::T;
+  const int G = p.group;
+  const int items = G * (D / 4);
+  int tpi = THREADS / items;
+  tpi = tpi >= 8 ? 8 : tpi >= 4 ? 4 : tpi >= 2 ? 2 : 1;
+  const int tid = threadIdx.x, sub = tid % tpi;
+  const int64_t base = pair * p.max_splits;
+  for (int it = tid / tpi; it < items; it += THREADS / tpi) {
+    // The lanes of a tpi group share `it`, so they run the same trip count
+    // and are all active at the butterfly below.
+    const int col = it / (D / 4), d4 = it % (D / 4);
+    float m = -INFINITY, l = 0.f;
+    floatx4 o = {0.f, 0.f, 0.f, 0.f};
+    for (int sp0 = sub; sp0 < nsplit; sp0 += 8 * tpi) {
+      float mb[8], lb[8];
+      floatx4 ob[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int sp = sp0 + k * tpi;
+        if (sp < nsplit) {
+          const int64_t pi = (base + sp) * G + col;
+          mb[k] = part_load(p.part_ml + 2 * pi);
+          lb[k] = part_load(p.part_ml + 2 * pi + 1);
+          const float* po = p.part_o + pi * D + 4 * d4;
+          ob[k] = floatx4{part_load(po), part_load(po + 1), part_load(po + 2), part_load(po + 3)};
+        } else {
+          mb[k] = -INFINITY;
+          lb[k] = 0.f;
+          ob[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) merge_into(m, l, o, mb[k], lb[k], ob[k]);
+    }
+    for (int off = 1; off < tpi; off <<= 1) {
+      const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
+      const floatx4 o2 = {__shfl_xor(o[0], off), __shfl_xor(o[1], off), __shfl_xor(o[2], off), __shfl_xor(o[3], off)};
+      merge_into(m, l, o, m2, l2, o2);
+    }
+    if (sub == 0) {
+      // A split that met an invalid block id carries NaN, which propagates.
+      const float inv = l > 0.f || l != l ? 1.f / l : 0.f;
+      typename DT::vec4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(o[r] * inv);
+      *reinterpret_cast<u32x2*>(out_row + col * D + 4 * d4) = __builtin_bit_cast(u32x2, v4);
+    }
+  }
+}
+
+template <class IDX>
+__device__ __forceinline__ int64_t ld_idx(const void* p, int64_t i) {
+  return static_cast<int64_t>(reinterpret_cast<const IDX*>(p)[i]);
+}
+
+template <class DT, int D, int W, int CH, class BTI>
+__global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
+  using Cfg = DecodeCfg<D, W, CH>;
   using T = typename DT::T;
   using V8 = typename DT::vec8;
-  constexpr int CH = Cfg::CH, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, VT_LD = Cfg::VT_LD;
+  constexpr int THREADS = Cfg::kThreads;
+  constexpr int NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, VT_LD = Cfg::VT_LD;
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
   __shared__ int s_last;
 
   const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int G = p.group, Hkv = p.num_kv_heads;
+  const int bs_mask = (1 << p.bs_shift) - 1;
+  const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
+  const int64_t t_split0 = static_cast<int64_t>(split) * p.split_tokens;
+  const int64_t t_cap = p.max_ctx < t_split0 + p.split_tokens ? p.max_ctx : t_split0 + p.split_tokens;
 
+  // Loads that do not depend on the context length go out together: the
+  // length, this wave's first block-table entries and (decode-only) Q.
+  const int64_t L_raw = load_index(p.seq_lens, s, p.sl64);
+  const int64_t tb0 = t_split0 + w * CH;
+  int64_t blk[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    // Clamped into the table so the load is unconditional; entries past the
+    // split are never used.
+    int64_t t = tb0 + 16 * j + c16;
+    t = t < t_cap ? t : t_cap - 1;
+    t = t > 0 ? t : 0;
+    blk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+  }
   int64_t qtok = s;
   if (!p.decode_only) {
     const int64_t q0 = load_index(p.qsl, s, p.qsl64);
@@ -88,28 +195,28 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
     qtok = q0;
   }
   if (qtok < 0 || qtok >= p.num_tokens) return;
-  int64_t L = load_index(p.seq_lens, s, p.sl64);
-  L = L < p.max_ctx ? L : p.max_ctx;
+  V8 qop[NC];
+  {
+    const int hq = c16 < G ? c16 : G - 1;  // in-row address for the padding columns
+    const T* qrow = reinterpret_cast<const T*>(p.query) +
+                    (qtok * p.num_heads + static_cast<int64_t>(kvh) * G + hq) * D;
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qop[c] = load16<DT>(qrow + 32 * c + 8 * g);
+    if (c16 >= G)
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qop[c] = zero8<DT>();
+  }
+
+  const int64_t L = L_raw < p.max_ctx ? L_raw : p.max_ctx;
   T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
-  const int64_t t_split0 = static_cast<int64_t>(split) * p.split_tokens;
   if (t_split0 >= L) {
     // No key is visible: the reference's masked softmax yields zeros.
     if (split == 0)
-      for (int i = tid; i < G * D; i += kThreads) out_row[i] = static_cast<T>(0.f);
+      for (int i = tid; i < G * D; i += THREADS) out_row[i] = static_cast<T>(0.f);
     return;
   }
   const int64_t t_split1 = L < t_split0 + p.split_tokens ? L : t_split0 + p.split_tokens;
   const int nsplit = static_cast<int>((L + p.split_tokens - 1) / p.split_tokens);
-  const int bs_mask = (1 << p.bs_shift) - 1;
-
-  // Q^T operand: column c16 is query head kvh*G + c16 (zero past the group).
-  V8 qop[NC];
-  {
-    const T* qrow = reinterpret_cast<const T*>(p.query) +
-                    (qtok * p.num_heads + static_cast<int64_t>(kvh) * G + c16) * D;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) qop[c] = c16 < G ? load16<DT>(qrow + 32 * c + 8 * g) : zero8<DT>();
-  }
 
   T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
   float m_run = -INFINITY, l_run = 0.f;
@@ -120,27 +227,34 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between slots
   const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
   const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
-  const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
 
-  for (int64_t tb = t_split0 + w * CH; tb < t_split1; tb += kWaves * CH) {
+  for (int64_t tb = tb0; tb < t_split1; tb += W * CH) {
     V8 kr[NT][NC], vr[NT][NC];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t t = tb + 16 * j + c16;
       bool valid = t < t_split1;
-      int64_t blk = 0;
-      if (valid) blk = load_index(p.bt, bt_row + (t >> p.bs_shift), p.bt64);
-      if (valid && (blk < 0 || blk >= p.num_blocks)) {
+      if (valid && (blk[j] < 0 || blk[j] >= p.num_blocks)) {
         bad = 1;
         valid = false;
       }
-      if (!valid) blk = 0;  // addresses are formed from in-range blocks only
-      const int64_t off = ((blk << p.bs_shift) + (t & bs_mask)) * slot_stride;
+      // Invalid lanes read slot 0 (always in bounds) and are zeroed below.
+      const int64_t off = valid ? ((blk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        kr[j][c] = valid ? load16<DT>(kbase + off + 32 * c) : zero8<DT>();
-        vr[j][c] = valid ? load16<DT>(vbase + off + 32 * c) : zero8<DT>();
+        kr[j][c] = load16<DT>(kbase + off + 32 * c);
+        vr[j][c] = load16<DT>(vbase + off + 32 * c);
       }
+      if (!valid)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) vr[j][c] = zero8<DT>();
+    }
+    // Next step's block-table entries travel while this step computes.
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      int64_t t = tb + W * CH + 16 * j + c16;
+      t = t < t_split1 ? t : t_split1 - 1;
+      blk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
     }
     // Stage V transposed (vt[dim][token]) for the PV operand.
 #pragma unroll
@@ -211,11 +325,11 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
   }
   l_run = group4_sum(l_run);
 
-  // Merge the four waves' (max, sum, O) through LDS.
+  // Merge the waves' (max, sum, O) through LDS.
   bad = __syncthreads_or(bad);
   float* red_o = reinterpret_cast<float*>(smem);
-  float* red_m = red_o + kWaves * 16 * D;
-  float* red_l = red_m + kWaves * 16;
+  float* red_m = red_o + W * 16 * D;
+  float* red_l = red_m + W * 16;
 #pragma unroll
   for (int n = 0; n < NN; ++n)
 #pragma unroll
@@ -228,14 +342,14 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
 
   const int nout = G * D;
   const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
-  for (int i = tid; i < nout; i += kThreads) {
+  for (int i = tid; i < nout; i += THREADS) {
     const int col = i / D, d = i - col * D;
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red_m[ww * 16 + col]);
+    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, red_m[ww * 16 + col]);
     float lsum = 0.f, o = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
+    for (int ww = 0; ww < W; ++ww) {
       const float mw = red_m[ww * 16 + col];
       if (mw != -INFINITY) {
         const float sc = fast_exp2(mw - M);
@@ -248,40 +362,28 @@ __global__ __launch_bounds__(kThreads) void paged_decode_kernel(AttnParams p) {
       out_row[i] = static_cast<T>(lsum > 0.f || lsum != lsum ? o / lsum : 0.f);
     } else {
       const int64_t pi = (pair * p.max_splits + split) * G + col;
-      p.part_o[pi * D + d] = o;
+      part_store(p.part_o + pi * D + d, o);
       if (d == 0) {
-        p.part_ml[pi * 2] = M;
-        p.part_ml[pi * 2 + 1] = lsum;
+        part_store(p.part_ml + 2 * pi, M);
+        part_store(p.part_ml + 2 * pi + 1, lsum);
       }
     }
   }
   if (nsplit == 1) return;
-
-  // Split-K merge inside the same launch: the last workgroup of this
-  // (sequence, kv head) to arrive combines every split's partial.
-  __threadfence();
+  // Split-K merge inside the same launch: the last workgroup of this pair to
+  // arrive combines every split's partial.  Partials are written and read
+  // with device-scope (sc1) accesses, which bypass the per-XCD L2s, so the
+  // only ordering needed is that this workgroup's stores are acknowledged
+  // before its arrival is counted.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   if (tid == 0) {
-    const unsigned prev = atomicAdd(&p.counters[pair], 1u);
+    const unsigned prev = __hip_atomic_fetch_add(&p.counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     s_last = prev == static_cast<unsigned>(nsplit - 1);
   }
   __syncthreads();
   if (!s_last) return;
-  __threadfence();
-  for (int i = tid; i < nout; i += kThreads) {
-    const int col = i / D, d = i - col * D;
-    const int64_t p0 = pair * p.max_splits * G + col;
-    float M = -INFINITY;
-    for (int sp = 0; sp < nsplit; ++sp) M = fmaxf(M, p.part_ml[(p0 + sp * G) * 2]);
-    float lsum = 0.f, o = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const int64_t pi = p0 + sp * G;
-      const float sc = fast_exp2(p.part_ml[pi * 2] - M);
-      lsum += p.part_ml[pi * 2 + 1] * sc;
-      o += p.part_o[pi * D + d] * sc;
-    }
-    out_row[i] = static_cast<T>(lsum > 0.f || lsum != lsum ? o / lsum : 0.f);
-  }
+  merge_splits<DT, D, THREADS>(p, pair, nsplit, out_row);
   if (tid == 0) __hip_atomic_store(&p.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -482,11 +584,17 @@ struct DecodePlan {
   int max_splits;
 };
 
-// Tokens per decode workgroup: the four waves' first step, doubled until a
+// Decode launch shape: kDecodeWaves waves per workgroup, each moving
+// decode_chunk<D> tokens (16 KiB of K+V) per step.
+constexpr int kDecodeWaves = 4;
+template <int D>
+constexpr int decode_chunk() { return D == 64 ? 64 : 32; }
+
+// Tokens per decode workgroup: one step of every wave, doubled until a
 // sequence needs at most 64 workgroups, which bounds the partial buffers
 // while giving short batches enough workgroups to cover 256 CUs.
 DecodePlan plan_decode(int head_dim, int64_t ctx_tokens) {
-  const int base = kWaves * (head_dim == 64 ? DecodeCfg<64>::CH : DecodeCfg<128>::CH);
+  const int base = kDecodeWaves * (head_dim == 64 ? decode_chunk<64>() : decode_chunk<128>());
   int64_t tok = base;
   while ((ctx_tokens + tok - 1) / tok > 64) tok *= 2;
   DecodePlan plan;
@@ -527,8 +635,12 @@ int64_t round_up_ctx(int max_seq_len, int block_size) {
 template <class DT, int D>
 hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipStream_t stream) {
   void* args[] = {&p};
-  hipError_t e = hipLaunchKernel(reinterpret_cast<const void*>(&paged_decode_kernel<DT, D>),
-                                 dim3(p.max_splits, p.num_kv_heads, num_seqs), dim3(kThreads),
+  constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
+  // The block-table width is a template argument so table loads need no
+  // per-lane branch.
+  const void* dk = p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t>)
+                          : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t>);
+  hipError_t e = hipLaunchKernel(dk, dim3(p.max_splits, p.num_kv_heads, num_seqs), dim3(W * 64),
                                  args, 0, stream);
   if (e != hipSuccess || p.decode_only) return e;
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;

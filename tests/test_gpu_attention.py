@@ -271,7 +271,11 @@ def test_repeated_calls_reuse_workspace():
 
 
 def test_graph_replays_match_eager():
-    """Capture decode calls in a HIP graph; every replay matches the eager result."""
+    """Capture decode calls in a HIP graph; every replay matches the eager result.
+
+    Eager calls run between replays, so the split-K counters a replay leaves
+    behind are exercised by the eager path and the other way round.
+    """
     case = make_case("c2", seed=5, device=DEV, gen_device=DEV)
     eager = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale).clone()
     torch.cuda.synchronize()
@@ -284,11 +288,15 @@ def test_graph_replays_match_eager():
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=s):
         out = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
-    for _ in range(4):
-        out.zero_()
-        graph.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(out, eager)
+    with torch.inference_mode():
+        for _ in range(4):
+            out.fill_(0)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            again = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager)
 
 
 def test_rejects_unsupported_shapes():
