@@ -4,12 +4,23 @@
 
 A step is one call of the paged-attention op on one batch (config c2 by
 default: decode, B=32, Qwen2.5-0.5B heads 14/2/64, block 16, fp16, lognormal
-contexts).  Inputs are resident in HBM before timing.  The op is called on R
-independent replicas (caches, tables, queries) whose combined footprint is
->= 1.2 GB, cycled in order, so KV is read from HBM and not from the 256 MB
-Infinity Cache.  The K timed calls are replayed from a HIP graph captured over
-the R replicas (a serving loop issues them the same way), bracketed by
-device synchronisation, and timed with HIP events on the launch stream.
+contexts).  Inputs are resident in HBM before timing.
+
+The calls are laid out the way the engine issues them: a serving step builds
+one AttentionMetadata (block tables, lengths) and every layer of the model
+calls attention with it on that layer's own K/V cache and queries
+(reference qwen2.py:105-113, model_runner.py:85-168).  So the benchmark holds
+several steps (different seeds, i.e. different length draws and block
+tables) of --layers calls each, every call with its own freshly drawn caches
+and queries; the caches of all calls together exceed 1.2 GB, so KV is always
+read from HBM and not from the 256 MB Infinity Cache.  A second pass gives
+every call its own metadata too (nothing shared, every table read cold) and is
+reported as `cold_metadata`.
+
+The K timed calls are replayed from a HIP graph captured over the calls (a
+serving loop issues them the same way), bracketed by device synchronisation,
+and timed with HIP events on the launch stream.  A decode batch is one kernel
+launch, so us per call is us per launch.
 
 Prints one JSON line: value = algorithmic KV GB/s (sum_i 2*L_i*Hkv*D*itemsize
 per call / time per call), plus us/call, % of the 8 TB/s HBM peak, the
@@ -21,7 +32,6 @@ from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import platform
 import statistics
@@ -30,7 +40,6 @@ import time
 
 METRIC = "paged-attn decode HBM GB/s (% of peak) + µs/call, B=32 Qwen-0.5B heads"
 HBM_PEAK_GBS = 8000.0
-MFMA_PEAK_TFLOPS = {"fp16": 2500.0, "bf16": 2500.0}
 
 WORKLOADS = {
     "c1": "decode B=8 ctx U[64,512] Hq14/Hkv2/D64 block16 fp16, 256-block pool",
@@ -49,23 +58,26 @@ def parse_args(argv=None):
     ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--block-size", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--layers", type=int, default=24,
+                    help="attention calls per serving step sharing one metadata (Qwen2.5-0.5B: 24)")
+    ap.add_argument("--min-steps", type=int, default=4, help="distinct serving steps (length draws)")
     ap.add_argument("--replica-gb", type=float, default=1.2,
-                    help="minimum combined footprint of the replicas cycled through")
+                    help="minimum combined K/V footprint of the calls cycled through")
+    ap.add_argument("--no-cold", action="store_true", help="skip the all-cold-metadata pass")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-calls", type=int, default=20)
     ap.add_argument("--eager", action="store_true", help="also time K eager (non-graph) calls")
     return ap.parse_args(argv)
 
 
-def _case_bytes(case) -> int:
-    t = [case.query, case.k_cache, case.v_cache, case.md.block_tables]
-    return sum(x.numel() * x.element_size() for x in t)
+def _kv_footprint(case) -> int:
+    return case.k_cache.numel() * case.k_cache.element_size() * 2
 
 
 def _cpu_baseline(case_gpu, calls, gpu_out):
     """Time the repo's torch gather+SDPA oracle on this host (bounded sample).
 
-    The sample is the benchmarked replica itself, copied to host memory, so
+    The sample is the first benchmarked call itself, copied to host memory, so
     the parity gate compares the GPU output with the oracle on identical inputs.
     """
     import torch
@@ -79,7 +91,7 @@ def _cpu_baseline(case_gpu, calls, gpu_out):
     md_cpu = AttentionMetadata(**{k: (v.cpu() if isinstance(v, torch.Tensor) else v)
                                   for k, v in md.__dict__.items()})
     q, kc, vc = case_gpu.query.cpu(), case_gpu.k_cache.cpu(), case_gpu.v_cache.cpu()
-    # Parity gate for the benchmarked replica: fp32-accumulated oracle vs the GPU output.
+    # Parity gate for the benchmarked call: fp32-accumulated oracle vs the GPU output.
     ref = paged_attention_ref(q, kc, vc, md_cpu, case_gpu.scale)
     err = (gpu_out.float().cpu() - ref).abs().max().item()
     for _ in range(3):
@@ -99,11 +111,97 @@ def _cpu_baseline(case_gpu, calls, gpu_out):
         "cores": cores,
         "kind": "port",
         "ms_per_call": med * 1e3,
-        "sample": f"{case_gpu.config} seed {case_gpu.seed} (the first benchmarked replica): median of "
+        "sample": f"{case_gpu.config} seed {case_gpu.seed} (the first benchmarked call): median of "
                   f"{len(ts)} calls after 3 warm-up, torch gather+SDPA in "
                   f"{str(q.dtype).replace('torch.', '')} on {torch.get_num_threads()} threads "
                   f"({platform.processor() or platform.machine()})",
     }, err
+
+
+def _build_calls(args, dev, shared):
+    """Calls to cycle through: steps of --layers calls sharing one metadata
+    (shared=True) or fully independent calls (shared=False)."""
+    from nanoserve_amd.workloads import make_case, make_layer
+
+    calls, total, step = [], 0, 0
+    while total < args.replica_gb * 1e9 or step < (args.min_steps if shared else 2):
+        base = make_case(args.config, seed=args.seed + step, device=dev, gen_device=dev,
+                         block_size=args.block_size)
+        for layer in range(args.layers if shared else 1):
+            c = base if layer == 0 else make_layer(base, seed=1000 * (args.seed + step) + layer, gen_device=dev)
+            calls.append(c)
+            total += _kv_footprint(c)
+        step += 1
+    return calls, total, step
+
+
+def _time_calls(torch, calls, news, K, warmup, stream):
+    """Warm up, capture all calls in one HIP graph, time K replayed calls."""
+    from nanoserve_amd import paged_attention_hip, reshape_and_cache
+
+    R = len(calls)
+
+    def attn(i):
+        c = calls[i]
+        return paged_attention_hip(c.query, c.k_cache, c.v_cache, c.md, c.scale)
+
+    def write(i):
+        c = calls[i]
+        reshape_and_cache(news[i][0], news[i][1], c.k_cache, c.v_cache, c.md.slot_mapping)
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        # Write-then-attend, as the model's call site does (reference
+        # qwen2.py:57-65): every call's new-token K/V goes in first.  Rewriting
+        # the same rows later leaves the caches unchanged.
+        for i in range(R):
+            write(i)
+        first_out = attn(0).clone()
+        for w in range(max(warmup, R)):
+            attn(w % R)
+    torch.cuda.synchronize()
+
+    def capture(fn, idxs):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            for i in idxs:
+                fn(i)
+        return g
+
+    full, rem = divmod(K, R)
+    g_attn = capture(attn, range(R))
+    g_rem = capture(attn, range(rem)) if rem else None
+    g_write = capture(write, range(R))
+
+    def timed(graph, graph_rem, reps):
+        with torch.cuda.stream(stream):
+            for _ in range(2):
+                graph.replay()
+            stream.synchronize()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            if graph_rem is not None:
+                graph_rem.replay()
+            end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) * 1e-3
+
+    t_attn = timed(g_attn, g_rem, full)
+    kv = [c.kv_bytes() for c in calls]
+    bytes_total = full * sum(kv) + sum(kv[:rem])
+    write_reps = max(1, K // R)
+    t_write = timed(g_write, None, write_reps)
+    del g_attn, g_rem, g_write
+    return {
+        "s_per_call": t_attn / K,
+        "gbs": bytes_total / t_attn / 1e9,
+        "write_us": t_write / (write_reps * R) * 1e6,
+        "kv_mean": sum(kv) / R,
+        "first_out": first_out,
+        "attn": attn,
+    }
 
 
 def main(argv=None):
@@ -115,103 +213,40 @@ def main(argv=None):
 
     import torch
 
-    from nanoserve_amd import paged_attention_hip, reshape_and_cache
-    from nanoserve_amd.workloads import make_case
-
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-
-    # ---- replicas ---------------------------------------------------------
-    cases, total = [], 0
-    while total < args.replica_gb * 1e9 or len(cases) < 2:
-        c = make_case(args.config, seed=args.seed + len(cases), device=dev, gen_device=dev,
-                      block_size=args.block_size)
-        cases.append(c)
-        total += _case_bytes(c)
-    R = len(cases)
-    dtype = cases[0].query.dtype
-    dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
-    kv_bytes = [c.kv_bytes() for c in cases]
-
-    # New-token K/V of each replica for the cache-write timing.
-    news = []
-    for c in cases:
-        g = torch.Generator(device=dev).manual_seed(c.seed + 100)
-        shape = (c.md.num_tokens, c.num_kv_heads, c.head_dim)
-        news.append((torch.randn(shape, generator=g, device=dev).to(dtype),
-                     torch.randn(shape, generator=g, device=dev).to(dtype)))
-
-    def attn(i):
-        c = cases[i]
-        return paged_attention_hip(c.query, c.k_cache, c.v_cache, c.md, c.scale)
-
-    def write(i):
-        c = cases[i]
-        reshape_and_cache(news[i][0], news[i][1], c.k_cache, c.v_cache, c.md.slot_mapping)
-
     stream = torch.cuda.Stream(dev)
-    stream.wait_stream(torch.cuda.current_stream(dev))
-    with torch.cuda.stream(stream):
-        # Write-then-attend, as the model's call site does: every replica's
-        # new-token K/V goes in first.  Rewriting the same rows later leaves
-        # the caches unchanged, so first_out stays the output of replica 0.
-        for i in range(R):
-            write(i)
-        first_out = attn(0).clone()
-        for w in range(max(args.warmup, R)):
-            attn(w % R)
-            write(w % R)
-    torch.cuda.current_stream(dev).wait_stream(stream)
-    torch.cuda.synchronize()
 
-    def capture(fn, idxs):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
-            for i in idxs:
-                fn(i)
-        return g
+    def new_tokens(calls):
+        out = []
+        for i, c in enumerate(calls):
+            g = torch.Generator(device=dev).manual_seed(1_000_003 + i)
+            shape = (c.md.num_tokens, c.num_kv_heads, c.head_dim)
+            out.append((torch.randn(shape, generator=g, device=dev).to(c.query.dtype),
+                        torch.randn(shape, generator=g, device=dev).to(c.query.dtype)))
+        return out
 
     K = args.steps
-    full, rem = divmod(K, R)
-    g_attn = capture(attn, range(R))
-    g_attn_rem = capture(attn, range(rem)) if rem else None
-    g_write = capture(write, range(R))
-
-    def timed(graph, graph_rem, reps):
-        for _ in range(2):
-            graph.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for _ in range(reps):
-            graph.replay()
-        if graph_rem is not None:
-            graph_rem.replay()
-        end.record()
-        end.synchronize()
-        torch.cuda.synchronize()
-        return start.elapsed_time(end) * 1e-3
-
-    t_attn = timed(g_attn, g_attn_rem, full)
-    bytes_total = full * sum(kv_bytes) + sum(kv_bytes[:rem])
-    s_per_call = t_attn / K
-    gbs = bytes_total / t_attn / 1e9
-
-    t_write = timed(g_write, None, max(1, K // R))
-    write_us = t_write / (max(1, K // R) * R) * 1e6
+    calls, total, nsteps = _build_calls(args, dev, shared=True)
+    dtype = calls[0].query.dtype
+    dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
+    res = _time_calls(torch, calls, new_tokens(calls), K, args.warmup, stream)
 
     eager_us = None
     if args.eager:
+        attn = res["attn"]
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for k in range(K):
-            attn(k % R)
+        with torch.cuda.stream(stream):
+            for k in range(K):
+                attn(k % len(calls))
         torch.cuda.synchronize()
         eager_us = (time.perf_counter() - t0) / K * 1e6
 
+    gbs, s_per_call = res["gbs"], res["s_per_call"]
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -227,14 +262,16 @@ def main(argv=None):
         "data": "synthetic",
         "config": {
             "workload": f"{args.config}: {WORKLOADS[args.config]}",
-            "block_size": cases[0].k_cache.shape[1],
-            "global_batch": cases[0].md.num_seqs,
-            "tokens_per_call": cases[0].md.num_tokens,
-            "replicas": R,
-            "replica_footprint_gb": round(total / 1e9, 3),
-            "seeds": f"{args.seed}..{args.seed + R - 1}",
-            "kv_bytes_per_call_mean": sum(kv_bytes) / R,
-            "timing": "HIP-graph replay of K calls cycling the replicas, hipEvents on the launch stream",
+            "block_size": calls[0].k_cache.shape[1],
+            "global_batch": calls[0].md.num_seqs,
+            "tokens_per_call": calls[0].md.num_tokens,
+            "serving_steps": nsteps,
+            "layers_per_step": args.layers,
+            "calls_cycled": len(calls),
+            "kv_footprint_gb": round(total / 1e9, 3),
+            "seeds": f"{args.seed}..{args.seed + nsteps - 1}",
+            "kv_bytes_per_call_mean": res["kv_mean"],
+            "timing": "HIP-graph replay of K calls cycling all steps x layers, hipEvents on the launch stream",
         },
         "us_per_call": round(s_per_call * 1e6, 3),
         "pct_of_peak": round(100.0 * gbs / HBM_PEAK_GBS, 2),
@@ -246,16 +283,32 @@ def main(argv=None):
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": None,
         },
-        "reshape_and_cache_us": round(write_us, 3),
+        "reshape_and_cache_us": round(res["write_us"], 3),
     }
     if args.config == "c3":
-        flops = sum(c.prefill_flops() for c in cases) / R
+        flops = sum(c.prefill_flops() for c in calls) / len(calls)
         result["prefill_flops_per_call"] = flops
         result["mfma_tflops"] = round(flops / s_per_call / 1e12, 2)
     if eager_us is not None:
         result["eager_us_per_call"] = round(eager_us, 2)
+    first_case, first_out = calls[0], res["first_out"]
+    del res
+
+    if not args.no_cold:
+        del calls
+        cold_args = argparse.Namespace(**vars(args))
+        cold, _, _ = _build_calls(cold_args, dev, shared=False)
+        r2 = _time_calls(torch, cold, new_tokens(cold), K, args.warmup, stream)
+        result["cold_metadata"] = {
+            "us_per_call": round(r2["s_per_call"] * 1e6, 3),
+            "gbs": round(r2["gbs"], 2),
+            "calls_cycled": len(cold),
+            "note": "every call with its own block tables and lengths (no step shares metadata)",
+        }
+        del cold, r2
+
     if not args.no_cpu_baseline:
-        cpu, err = _cpu_baseline(cases[0], args.cpu_calls, first_out)
+        cpu, err = _cpu_baseline(first_case, args.cpu_calls, first_out)
         result["cpu_baseline"] = cpu
         result["max_abs_err_vs_oracle"] = err
         tol = 2e-3 if dtype == torch.float16 else 1e-2

@@ -106,6 +106,14 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  * reference decode fast path.  Otherwise query_start_loc delimits each
  * sequence's query rows; sequences with an empty query range are skipped.
  *
+ * seq_lens_host (optional, may be NULL) is a HOST copy of seq_lens -- the
+ * reference's AttentionMetadata.seq_lens_cpu (attention.py:52-54), which its
+ * non-decode path already treats as authoritative (attention.py:124).  For a
+ * decode-only batch it lets the library launch exactly one workgroup per
+ * (sequence, kv head, context split), longest sequences first, instead of a
+ * grid sized by max_seq_len.  It must equal seq_lens; a device length longer
+ * than the host copy makes that sequence's outputs NaN.
+ *
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
  * Supported: head_dim in {64, 128}; block_size a power of two in [8, 256];
  * num_heads / num_kv_heads <= 16.  Loops are bounded by each sequence's
@@ -119,6 +127,7 @@ int ns_paged_attention(void* out, const void* query,
                        int64_t block_table_width, int block_tables_is_int64,
                        const void* seq_lens, int seq_lens_is_int64,
                        const void* query_start_loc, int query_start_loc_is_int64,
+                       const void* seq_lens_host, int seq_lens_host_is_int64,
                        int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
                        int is_decode_only,
                        int num_heads, int num_kv_heads, int head_dim,

@@ -15,6 +15,7 @@ torch or Triton fallback; a missing library or an unsupported shape raises.
 
 from __future__ import annotations
 
+import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -138,6 +139,14 @@ def paged_attention_hip(
         qsl = _index(md.query_start_loc, "query_start_loc", device).contiguous()
         qsl_ptr, qsl64 = qsl.data_ptr(), int(qsl.dtype == torch.int64)
 
+    # The host copy of the lengths lets the library size the decode grid
+    # exactly (one workgroup per split, longest sequences first).
+    lens_host = None
+    if md.seq_lens_cpu is not None:
+        if len(md.seq_lens_cpu) < md.num_seqs:
+            raise ValueError("seq_lens_cpu is shorter than num_seqs")
+        lens_host = (ctypes.c_int64 * md.num_seqs)(*md.seq_lens_cpu[:md.num_seqs])
+
     stream = torch.cuda.current_stream(device).cuda_stream
     nbytes = lib.ns_paged_attention_workspace_size(
         md.num_seqs, num_heads, num_kv_heads, head_dim, block_size,
@@ -153,6 +162,7 @@ def paged_attention_hip(
         bt.data_ptr(), bt.stride(0), bt.shape[1], int(bt.dtype == torch.int64),
         sl.data_ptr(), int(sl.dtype == torch.int64),
         qsl_ptr, qsl64,
+        lens_host, 1,
         md.num_seqs, num_tokens, md.max_query_len, md.max_seq_len, int(decode_only),
         num_heads, num_kv_heads, head_dim, block_size, num_blocks,
         float(scale), _lib.DTYPE_CODES[q.dtype],

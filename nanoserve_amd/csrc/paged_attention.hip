@@ -18,6 +18,10 @@
 // between lanes.  V^T is staged through LDS.
 #include <math.h>
 
+#include <algorithm>
+#include <utility>
+#include <vector>
+
 #include "ns_common.h"
 
 namespace ns {
@@ -25,6 +29,8 @@ namespace {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
+// Plan entries carried in the kernel arguments (keeps them under 4 KiB).
+constexpr int kPlanMax = 768;
 
 struct AttnParams {
   char* out;
@@ -48,7 +54,12 @@ struct AttnParams {
   int skip_decode_rows;   // varlen: one-row sequences belong to the decode kernel
   float* part_o;          // [S, Hkv, max_splits, G, D]  unnormalised partial outputs
   float* part_ml;         // [S, Hkv, max_splits, G, 2]  (running max, running sum)
+  int part_o_bytes, part_ml_bytes;
   unsigned* counters;     // [S, Hkv] arrivals per (sequence, kv head); left at zero
+  int plan_n;             // decode workgroups listed in plan (0: no plan)
+  // Decode schedule from host-side lengths: entry y = s | split << 16 | nsplit << 24,
+  // longest sequences first.
+  uint32_t plan[kPlanMax];
 };
 
 // --------------------------------------------------------------------------
@@ -68,20 +79,39 @@ struct DecodeCfg {
   static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
 };
 
-// Partial results of split sp of pair (sequence, kv head) live in the
-// workspace as part_ml[2 * ((pair * max_splits + sp) * G + col) + {0, 1}] =
-// (running max, running sum) and part_o[((pair * max_splits + sp) * G + col) * D + d].
+// Split-K partials.  Split sp of pair (sequence, kv head) stores, for each
+// query head col of the group, its running (max, sum) at
+//   part_ml[2 * ((pair * max_splits + sp) * G + col) + {0, 1}]
+// and its unnormalised output at
+//   part_o[((pair * max_splits + sp) * G + col) * D + d].
 //
-// They cross workgroups (and XCDs, whose L2s are not coherent with each
-// other) through device-scope atomic accesses: the stores write through to
-// the device coherence point and the loads bypass the non-coherent caches, so
-// ordering the stores before the arrival counter (s_waitcnt) is all the
-// synchronisation the merge needs; no L2 writeback or invalidate is issued.
-__device__ __forceinline__ float part_load(const float* q) {
-  return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
+// other) through device-scope (sc1) buffer accesses: the stores write through
+// to the device coherence point and the loads bypass the non-coherent caches,
+// so the only ordering the merge needs is that a workgroup's stores are
+// acknowledged (s_waitcnt vmcnt(0)) before its arrival is counted.  No L2
+// writeback or invalidate is issued.
+constexpr int kSc1 = 16;                      // cache-policy bit SC1 of gfx94x/gfx950 buffer ops
+constexpr int kBufferWord3 = 0x00020000;      // raw 32-bit buffer descriptor, word 3
+
+struct PartBuffers {
+  __amdgpu_buffer_rsrc_t ml, o;
+};
+
+// 32-bit device-scope buffer load.  Wider partial loads are written as runs
+// of these, which the backend merges into dwordx2/x4: with ROCm 7.2's clang,
+// taking elements of a raw_buffer_load_b64/b128 result was miscompiled into a
+// single dword load at the base offset (both halves of a b64 read the same
+// dword), while b32 loads merge and narrow correctly.
+__device__ __forceinline__ float ld_sc1(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kSc1));
 }
-__device__ __forceinline__ void part_store(float* q, float v) {
-  __hip_atomic_store(q, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+__device__ __forceinline__ PartBuffers part_buffers(const AttnParams& p) {
+  PartBuffers b;
+  b.ml = __builtin_amdgcn_make_buffer_rsrc(p.part_ml, static_cast<short>(0), p.part_ml_bytes, kBufferWord3);
+  b.o = __builtin_amdgcn_make_buffer_rsrc(p.part_o, static_cast<short>(0), p.part_o_bytes, kBufferWord3);
+  return b;
 }
 
 __device__ __forceinline__ void merge_into(float& m, float& l, floatx4& o, float m2, float l2, floatx4 o2) {
@@ -94,12 +124,13 @@ __device__ __forceinline__ void merge_into(float& m, float& l, floatx4& o, float
 }
 
 // Combine the nsplit partials of one pair into out_row ([G, D] of this kv
-// head's query heads).  All THREADS threads take part; each float4 column
-// (head, 4 dims) is owned by tpi consecutive lanes that walk disjoint split
-// subsets with up to 8 loads in flight, then merge by butterfly, so the
-// result does not depend on timing.
+// head's query heads).  Each float4 column (head, 4 dims) is owned by tpi
+// consecutive lanes that walk disjoint split subsets with up to 8 loads in
+// flight each, then merge by butterfly; the order of operations is fixed, so
+// the result does not depend on timing.
 template <class DT, int D, int THREADS>
-__device__ void merge_splits(const AttnParams& p, int64_t pair, int nsplit, typename DT::T* out_row) {
+__device__ void merge_splits(const AttnParams& p, const PartBuffers& pb, int64_t pair, int nsplit,
+                             typename DT::T* out_row) {
   using T = typename DT::T;
   const int G = p.group;
   const int items = G * (D / 4);
@@ -118,21 +149,17 @@ __device__ void merge_splits(const AttnParams& p, int64_t pair, int nsplit, type
       floatx4 ob[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        const int sp = sp0 + k * tpi;
-        if (sp < nsplit) {
-          const int64_t pi = (base + sp) * G + col;
-          mb[k] = part_load(p.part_ml + 2 * pi);
-          lb[k] = part_load(p.part_ml + 2 * pi + 1);
-          const float* po = p.part_o + pi * D + 4 * d4;
-          ob[k] = floatx4{part_load(po), part_load(po + 1), part_load(po + 2), part_load(po + 3)};
-        } else {
-          mb[k] = -INFINITY;
-          lb[k] = 0.f;
-          ob[k] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
+        // Slots past nsplit read split 0 again (in bounds) and are dropped below.
+        const int sp = sp0 + k * tpi < nsplit ? sp0 + k * tpi : 0;
+        const int pi = static_cast<int>((base + sp) * G + col);
+        mb[k] = ld_sc1(pb.ml, pi * 8);
+        lb[k] = ld_sc1(pb.ml, pi * 8 + 4);
+        const int oo = pi * (D * 4) + 16 * d4;
+        ob[k] = floatx4{ld_sc1(pb.o, oo), ld_sc1(pb.o, oo + 4), ld_sc1(pb.o, oo + 8), ld_sc1(pb.o, oo + 12)};
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) merge_into(m, l, o, mb[k], lb[k], ob[k]);
+      for (int k = 0; k < 8; ++k)
+        if (sp0 + k * tpi < nsplit) merge_into(m, l, o, mb[k], lb[k], ob[k]);
     }
     for (int off = 1; off < tpi; off <<= 1) {
       const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
@@ -155,6 +182,11 @@ __device__ __forceinline__ int64_t ld_idx(const void* p, int64_t i) {
   return static_cast<int64_t>(reinterpret_cast<const IDX*>(p)[i]);
 }
 
+// Decode.  Work unit: (sequence s, kv head, split) = split_tokens consecutive
+// context tokens of one kv head, read once and used by all G query heads of
+// the group.  With a host plan the grid is (Hkv, plan_n) and plan entry y
+// names (s, split, nsplit), longest sequences first; otherwise the grid is
+// (max_splits, Hkv, S) and splits past a sequence's end exit at once.
 template <class DT, int D, int W, int CH, class BTI>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   using Cfg = DecodeCfg<D, W, CH>;
@@ -165,7 +197,18 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
   __shared__ int s_last;
 
-  const int split = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
+  int s, split, kvh, nsplit_plan = 0;
+  if (p.plan_n > 0) {
+    const uint32_t e = p.plan[blockIdx.y];
+    s = static_cast<int>(e & 0xFFFFu);
+    split = static_cast<int>((e >> 16) & 0xFFu);
+    nsplit_plan = static_cast<int>(e >> 24);
+    kvh = blockIdx.x;
+  } else {
+    split = blockIdx.x;
+    kvh = blockIdx.y;
+    s = blockIdx.z;
+  }
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int G = p.group, Hkv = p.num_kv_heads;
   const int bs_mask = (1 << p.bs_shift) - 1;
@@ -209,21 +252,28 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 
   const int64_t L = L_raw < p.max_ctx ? L_raw : p.max_ctx;
   T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
-  if (t_split0 >= L) {
-    // No key is visible: the reference's masked softmax yields zeros.
-    if (split == 0)
+  const int nsplit_len = static_cast<int>((L + p.split_tokens - 1) / p.split_tokens);
+  // The splits that arrive at this pair's merge.  A plan fixes them from the
+  // host lengths, so every launched workgroup arrives even if the device
+  // length is shorter; a device length the plan does not cover is a broken
+  // contract and poisons the pair with NaN.
+  int bad = 0;
+  int nsplit = nsplit_len;
+  if (p.plan_n > 0) {
+    bad = nsplit_len > nsplit_plan;
+    nsplit = nsplit_plan;
+  } else if (split >= nsplit_len) {
+    if (split == 0)  // no key is visible: the reference's masked softmax yields zeros
       for (int i = tid; i < G * D; i += THREADS) out_row[i] = static_cast<T>(0.f);
     return;
   }
   const int64_t t_split1 = L < t_split0 + p.split_tokens ? L : t_split0 + p.split_tokens;
-  const int nsplit = static_cast<int>((L + p.split_tokens - 1) / p.split_tokens);
 
   T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  int bad = 0;
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between slots
   const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
   const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
@@ -340,42 +390,48 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   }
   __syncthreads();
 
-  const int nout = G * D;
+  // One float4 of the workgroup's output per thread: (head col, dims 4*d4..+3).
   const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
-  for (int i = tid; i < nout; i += THREADS) {
-    const int col = i / D, d = i - col * D;
+  const PartBuffers pbuf = part_buffers(p);
+  for (int it = tid; it < G * (D / 4); it += THREADS) {
+    const int col = it / (D / 4), d4 = it % (D / 4);
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < W; ++ww) M = fmaxf(M, red_m[ww * 16 + col]);
-    float lsum = 0.f, o = 0.f;
+    float lsum = 0.f;
+    floatx4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < W; ++ww) {
       const float mw = red_m[ww * 16 + col];
       if (mw != -INFINITY) {
         const float sc = fast_exp2(mw - M);
         lsum += red_l[ww * 16 + col] * sc;
-        o += red_o[(ww * 16 + col) * D + d] * sc;
+        o += *reinterpret_cast<const floatx4*>(red_o + (ww * 16 + col) * D + 4 * d4) * sc;
       }
     }
-    if (bad) lsum = o = NAN;
+    if (bad) {
+      lsum = NAN;
+      o = floatx4{NAN, NAN, NAN, NAN};
+    }
     if (nsplit == 1) {
-      out_row[i] = static_cast<T>(lsum > 0.f || lsum != lsum ? o / lsum : 0.f);
+      const float inv = lsum > 0.f || lsum != lsum ? 1.f / lsum : 0.f;
+      typename DT::vec4 v4;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(o[r] * inv);
+      *reinterpret_cast<u32x2*>(out_row + col * D + 4 * d4) = __builtin_bit_cast(u32x2, v4);
     } else {
-      const int64_t pi = (pair * p.max_splits + split) * G + col;
-      part_store(p.part_o + pi * D + d, o);
-      if (d == 0) {
-        part_store(p.part_ml + 2 * pi, M);
-        part_store(p.part_ml + 2 * pi + 1, lsum);
-      }
+      const int pi = static_cast<int>((pair * p.max_splits + split) * G + col);
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), pbuf.o, pi * (D * 4) + 16 * d4, 0, kSc1);
+      if (d4 == 0)
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, M), __builtin_bit_cast(uint32_t, lsum)},
+                                              pbuf.ml, pi * 8, 0, kSc1);
     }
   }
   if (nsplit == 1) return;
+
   // Split-K merge inside the same launch: the last workgroup of this pair to
-  // arrive combines every split's partial.  Partials are written and read
-  // with device-scope (sc1) accesses, which bypass the per-XCD L2s, so the
-  // only ordering needed is that this workgroup's stores are acknowledged
-  // before its arrival is counted.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  // arrive combines every split's partial.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are acknowledged
   __syncthreads();
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(&p.counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -383,7 +439,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   }
   __syncthreads();
   if (!s_last) return;
-  merge_splits<DT, D, THREADS>(p, pair, nsplit, out_row);
+  merge_splits<DT, D, THREADS>(p, pbuf, pair, nsplit, out_row);
   if (tid == 0) __hip_atomic_store(&p.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -640,8 +696,9 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   // per-lane branch.
   const void* dk = p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t>)
                           : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t>);
-  hipError_t e = hipLaunchKernel(dk, dim3(p.max_splits, p.num_kv_heads, num_seqs), dim3(W * 64),
-                                 args, 0, stream);
+  const dim3 grid = p.plan_n > 0 ? dim3(p.num_kv_heads, p.plan_n, 1)
+                                 : dim3(p.max_splits, p.num_kv_heads, num_seqs);
+  hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
   if (e != hipSuccess || p.decode_only) return e;
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
   const int64_t nblk = (cols + VarlenCfg<D>::COLS - 1) / VarlenCfg<D>::COLS;
@@ -652,6 +709,35 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
 }
 
 bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
+
+// Fill p.plan from host-side context lengths: every (sequence, split) of a
+// decode batch, longest sequences first, so the splits whose merge is
+// largest start streaming first and their merges overlap the rest of the
+// launch.  Returns the entry count, or 0 when the batch does not fit the
+// plan (the launch then uses the full (max_splits, Hkv, S) grid).
+int build_decode_plan(AttnParams& p, const void* lens, int lens64, int num_seqs) {
+  if (num_seqs > 0xFFFF || p.max_splits > 0xFF) return 0;
+  std::vector<std::pair<int64_t, int>> order(num_seqs);
+  int64_t total = 0;
+  for (int i = 0; i < num_seqs; ++i) {
+    int64_t L = lens64 ? static_cast<const int64_t*>(lens)[i] : static_cast<const int32_t*>(lens)[i];
+    L = L < 0 ? 0 : (L < p.max_ctx ? L : p.max_ctx);
+    order[i] = {L, i};
+    const int64_t n = (L + p.split_tokens - 1) / p.split_tokens;
+    total += n < 1 ? 1 : n;
+  }
+  if (total > kPlanMax) return 0;
+  std::stable_sort(order.begin(), order.end(),
+                   [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a.first > b.first; });
+  int n_out = 0;
+  for (const auto& [L, i] : order) {
+    int64_t n = (L + p.split_tokens - 1) / p.split_tokens;
+    n = n < 1 ? 1 : n;
+    for (int64_t sp = 0; sp < n; ++sp)
+      p.plan[n_out++] = static_cast<uint32_t>(i) | static_cast<uint32_t>(sp) << 16 | static_cast<uint32_t>(n) << 24;
+  }
+  return n_out;
+}
 
 }  // namespace
 }  // namespace ns
@@ -689,6 +775,7 @@ extern "C" int ns_paged_attention(void* out, const void* query,
                                   int64_t block_table_width, int block_tables_is_int64,
                                   const void* seq_lens, int seq_lens_is_int64,
                                   const void* query_start_loc, int query_start_loc_is_int64,
+                                  const void* seq_lens_host, int seq_lens_host_is_int64,
                                   int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
                                   int is_decode_only,
                                   int num_heads, int num_kv_heads, int head_dim,
@@ -720,6 +807,8 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   const DecodePlan plan = plan_decode(head_dim, ctx_plan);
   const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan);
   if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
+  // Partials are addressed through buffer descriptors with 32-bit offsets.
+  if (wl.total - wl.o_off > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
 
   AttnParams p;
   p.out = static_cast<char*>(out);
@@ -750,6 +839,11 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   p.counters = reinterpret_cast<unsigned*>(ws + wl.counters_off);
   p.part_ml = reinterpret_cast<float*>(ws + wl.ml_off);
   p.part_o = reinterpret_cast<float*>(ws + wl.o_off);
+  p.part_ml_bytes = static_cast<int>(wl.o_off - wl.ml_off);
+  p.part_o_bytes = static_cast<int>(wl.total - wl.o_off);
+  p.plan_n = 0;
+  if (seq_lens_host && is_decode_only)
+    p.plan_n = build_decode_plan(p, seq_lens_host, seq_lens_host_is_int64, num_seqs);
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;

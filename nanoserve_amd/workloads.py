@@ -23,6 +23,7 @@ so slots a sequence does not own behave like stale KV.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass
 
@@ -162,6 +163,19 @@ def make_case(config: str, seed: int = 0, device="cpu", block_size: int | None =
     md = metadata_for(seq_lens, query_lens, tables, bs, device, index_dtype)
     return PagedCase(config, seed, query, k_cache, v_cache, md, 1.0 / math.sqrt(d),
                      list(seq_lens), list(query_lens), tables)
+
+
+def make_layer(case: PagedCase, seed: int, gen_device="cpu") -> PagedCase:
+    """Another layer of the same serving step: fresh queries and K/V caches of
+    the same shapes, the same metadata (block tables, lengths, slots)."""
+    g = torch.Generator(device=gen_device).manual_seed(seed)
+
+    def like(t: torch.Tensor) -> torch.Tensor:
+        return torch.randn(t.shape, generator=g, device=gen_device, dtype=torch.float32).to(
+            device=t.device, dtype=t.dtype)
+
+    return dataclasses.replace(case, query=like(case.query), k_cache=like(case.k_cache),
+                               v_cache=like(case.v_cache))
 
 
 def metadata_for(seq_lens: list[int], query_lens: list[int], tables: list[list[int]],

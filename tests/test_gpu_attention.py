@@ -151,6 +151,54 @@ def test_decode_wider_table_and_larger_max_seq_len():
     _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
+def test_decode_plan_and_full_grid_agree_bitwise():
+    """With seq_lens_cpu the library launches one workgroup per split (longest
+    first); without it the grid is sized by max_seq_len.  Same arithmetic, same
+    merge order: identical bits."""
+    seqs = [5, 300, 4000, 77, 1, 2048, 0]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16)
+    md_nolist = make_md(seqs, [1] * len(seqs), tables, 16, with_cpu_lists=False)
+    a = _run(q, kc, vc, md, 0.125)
+    b = _run(q, kc, vc, md_nolist, 0.125)
+    assert torch.equal(a, b)
+    _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+
+
+def test_decode_plan_overflow_falls_back_to_full_grid():
+    """More (sequence, split) units than the plan holds: the full grid runs."""
+    seqs = [2000 + 7 * i for i in range(100)]  # 100 x 8 splits > 768 plan entries
+    q, kc, vc, md, _, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=3)
+    _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+
+
+def test_decode_host_lengths_shorter_than_device_poison_only_that_sequence():
+    """A device length the host plan does not cover is a broken contract: that
+    sequence's rows are NaN, the others are right, and the split-K counters are
+    left clean for the next call."""
+    seqs = [300, 1000, 50]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * 3, 14, 2, 64, 16, torch.float16)
+    ref = paged_attention_ref(q, kc, vc, md, 0.125)
+    bad = make_md(seqs, [1] * 3, tables, 16)
+    bad.seq_lens_cpu = [300, 600, 50]
+    got = _run(q, kc, vc, bad, 0.125)
+    assert torch.isnan(got[1]).all()
+    _assert_close(got[[0, 2]], ref[[0, 2]], torch.float16)
+    _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
+    _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
+
+
+def test_decode_host_lengths_longer_than_device_follow_the_device():
+    """Extra planned splits past the device length contribute nothing."""
+    seqs = [300, 1000, 50]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * 3, 14, 2, 64, 16, torch.float16)
+    ref = paged_attention_ref(q, kc, vc, md, 0.125)
+    longer = make_md([300, 1500, 50], [1] * 3, [t + [0] * 40 for t in tables], 16)
+    longer.seq_lens = md.seq_lens
+    got = _run(q, kc, vc, longer, 0.125)
+    _assert_close(got, ref, torch.float16)
+    _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
+
+
 # ---- benchmark configurations ---------------------------------------------------------
 @pytest.mark.parametrize("seed", [0, 1])
 @pytest.mark.parametrize("config", ["c1", "c2"])
