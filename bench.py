@@ -67,7 +67,38 @@ def parse_args(argv=None):
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-calls", type=int, default=20)
     ap.add_argument("--eager", action="store_true", help="also time K eager (non-graph) calls")
+    ap.add_argument("--copy-calibration", type=float, default=None, metavar="MB",
+                    help="only run 5 plain device copies of MB megabytes (the known-size kernel that "
+                         "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings) and exit")
     return ap.parse_args(argv)
+
+
+def _copy_calibration(torch, mb):
+    n = int(mb * 1e6) // 16 * 16
+    src = torch.randint(0, 255, (n,), dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes": n, "kib": n / 1024, "copies": 5}))
+    return 0
+
+
+def _profiled_traffic(args):
+    """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE for
+    this exact workload (profiles/paged_decode_<config>_traffic.md), or None."""
+    if args.seed != 0 or args.block_size is not None or args.layers != 24 or args.min_steps != 4:
+        return None, None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"paged_decode_{args.config}_traffic.md")
+    if not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("machine-readable:"):
+            kv = dict(tok.split("=") for tok in line.split(":", 1)[1].split())
+            return int(kv["traffic_bytes_per_launch"]), os.path.relpath(path, os.path.dirname(path) + "/..")
+    return None, None
 
 
 def _kv_footprint(case) -> int:
@@ -218,6 +249,8 @@ def main(argv=None):
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration is not None:
+        return _copy_calibration(torch, args.copy_calibration)
     stream = torch.cuda.Stream(dev)
 
     def new_tokens(calls):
@@ -247,6 +280,7 @@ def main(argv=None):
         eager_us = (time.perf_counter() - t0) / K * 1e6
 
     gbs, s_per_call = res["gbs"], res["s_per_call"]
+    traffic, traffic_src = _profiled_traffic(args)
     result = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -281,10 +315,12 @@ def main(argv=None):
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "reshape_and_cache_us": round(res["write_us"], 3),
     }
+    if traffic is not None:
+        result["roofline"]["traffic_source"] = f"{traffic_src} (FETCH_SIZE x2.0 + WRITE_SIZE x1.0, copy-calibrated)"
     if args.config == "c3":
         flops = sum(c.prefill_flops() for c in calls) / len(calls)
         result["prefill_flops_per_call"] = flops
