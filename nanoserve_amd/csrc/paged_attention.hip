@@ -31,6 +31,7 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 // Plan entries carried in the kernel arguments (keeps them under 4 KiB).
 constexpr int kPlanMax = 768;
+constexpr uint32_t kPlanEmpty = 0xFFFFFFFFu;  // plan slot with no work (sequence ids stay below 0xFFFF)
 
 struct AttnParams {
   char* out;
@@ -57,8 +58,8 @@ struct AttnParams {
   int part_o_bytes, part_ml_bytes;
   unsigned* counters;     // [S, Hkv] arrivals per (sequence, kv head); left at zero
   int plan_n;             // decode workgroups listed in plan (0: no plan)
-  // Decode schedule from host-side lengths: entry y = s | split << 16 | nsplit << 24,
-  // longest sequences first.
+  // Decode schedule from host-side lengths: entry x = s | kvh << 16 | split << 20 |
+  // (nsplit - 1) << 26 for workgroup x, or kPlanEmpty.
   uint32_t plan[kPlanMax];
 };
 
@@ -184,10 +185,13 @@ __device__ __forceinline__ int64_t ld_idx(const void* p, int64_t i) {
 
 // Decode.  Work unit: (sequence s, kv head, split) = split_tokens consecutive
 // context tokens of one kv head, read once and used by all G query heads of
-// the group.  With a host plan the grid is (Hkv, plan_n) and plan entry y
-// names (s, split, nsplit), longest sequences first; otherwise the grid is
-// (max_splits, Hkv, S) and splits past a sequence's end exit at once.
-template <class DT, int D, int W, int CH, class BTI>
+// the group.  With a host plan the grid is (plan_n) and entry x names
+// (s, kv head, split, nsplit): all splits of a pair sit on workgroup ids with
+// the same x % 8, i.e. on one XCD, so the merging workgroup reads the
+// partials from its own L2 (the protocol does not depend on that placement,
+// only its speed does).  Otherwise the grid is (max_splits, Hkv, S) and splits
+// past a sequence's end exit at once.
+template <class DT, int D, int W, int CH, class BTI, bool PIPE>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   using Cfg = DecodeCfg<D, W, CH>;
   using T = typename DT::T;
@@ -199,11 +203,12 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 
   int s, split, kvh, nsplit_plan = 0;
   if (p.plan_n > 0) {
-    const uint32_t e = p.plan[blockIdx.y];
+    const uint32_t e = p.plan[blockIdx.x];
+    if (e == kPlanEmpty) return;
     s = static_cast<int>(e & 0xFFFFu);
-    split = static_cast<int>((e >> 16) & 0xFFu);
-    nsplit_plan = static_cast<int>(e >> 24);
-    kvh = blockIdx.x;
+    kvh = static_cast<int>((e >> 16) & 0xFu);
+    split = static_cast<int>((e >> 20) & 0x3Fu);
+    nsplit_plan = static_cast<int>(e >> 26) + 1;
   } else {
     split = blockIdx.x;
     kvh = blockIdx.y;
@@ -278,34 +283,67 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
   const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
 
-  for (int64_t tb = tb0; tb < t_split1; tb += W * CH) {
-    V8 kr[NT][NC], vr[NT][NC];
+  // Issue the K/V loads of the step starting at token tb: returns, per
+  // 16-token tile, whether this lane's token is valid (its V is zeroed at
+  // use, so nothing here waits for the data).  Invalid lanes read slot 0,
+  // which is always in bounds.
+  auto issue_step = [&](int64_t tb, const int64_t (&bk)[NT], V8 (&kx)[NT][NC], V8 (&vx)[NT][NC]) {
+    int vmask = 0;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t t = tb + 16 * j + c16;
       bool valid = t < t_split1;
-      if (valid && (blk[j] < 0 || blk[j] >= p.num_blocks)) {
+      if (valid && (bk[j] < 0 || bk[j] >= p.num_blocks)) {
         bad = 1;
         valid = false;
       }
-      // Invalid lanes read slot 0 (always in bounds) and are zeroed below.
-      const int64_t off = valid ? ((blk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
+      const int64_t off = valid ? ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        kr[j][c] = load16<DT>(kbase + off + 32 * c);
-        vr[j][c] = load16<DT>(vbase + off + 32 * c);
+        kx[j][c] = load16<DT>(kbase + off + 32 * c);
+        vx[j][c] = load16<DT>(vbase + off + 32 * c);
       }
-      if (!valid)
-#pragma unroll
-        for (int c = 0; c < NC; ++c) vr[j][c] = zero8<DT>();
+      vmask |= valid ? 1 << j : 0;
     }
-    // Next step's block-table entries travel while this step computes.
+    return vmask;
+  };
+  // Block-table entries of the step at tb (clamped into this split).
+  auto table_step = [&](int64_t tb, int64_t (&bk)[NT]) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      int64_t t = tb + W * CH + 16 * j + c16;
+      int64_t t = tb + 16 * j + c16;
       t = t < t_split1 ? t : t_split1 - 1;
-      blk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+      bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
     }
+  };
+
+  // Software pipeline over the wave's steps: step i+1's K/V loads and step
+  // i+2's table entries are in flight while step i computes.
+  V8 kr[NT][NC], vr[NT][NC];
+  int vmask = 0;
+  if (tb0 < t_split1) {
+    vmask = issue_step(tb0, blk, kr, vr);
+    table_step(tb0 + W * CH, blk);
+  }
+  for (int64_t tb = tb0; tb < t_split1; tb += W * CH) {
+    if (!PIPE && tb != tb0) {
+      // Without the pipeline (one step per wave in the common case) later
+      // steps issue their loads at the top of the step.
+      vmask = issue_step(tb, blk, kr, vr);
+      table_step(tb + W * CH, blk);
+    }
+    const bool has_next = PIPE && tb + W * CH < t_split1;
+    V8 kn[NT][NC], vn[NT][NC];
+    int vmask_n = 0;
+    if (has_next) {
+      vmask_n = issue_step(tb + W * CH, blk, kn, vn);
+      table_step(tb + 2 * W * CH, blk);
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      if (!(vmask >> j & 1))
+#pragma unroll
+        for (int c = 0; c < NC; ++c) vr[j][c] = zero8<DT>();
     // Stage V transposed (vt[dim][token]) for the PV operand.
 #pragma unroll
     for (int j = 0; j < NT; ++j)
@@ -372,6 +410,16 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
       }
     }
     wave_lds_sync();
+    if (has_next) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+          kr[j][c] = kn[j][c];
+          vr[j][c] = vn[j][c];
+        }
+      vmask = vmask_n;
+    }
   }
   l_run = group4_sum(l_run);
 
@@ -694,10 +742,16 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
   // The block-table width is a template argument so table loads need no
   // per-lane branch.
-  const void* dk = p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t>)
-                          : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t>);
-  const dim3 grid = p.plan_n > 0 ? dim3(p.num_kv_heads, p.plan_n, 1)
-                                 : dim3(p.max_splits, p.num_kv_heads, num_seqs);
+  // Workgroups whose waves take several steps pipeline their K/V loads
+  // (double-buffered registers, fewer resident waves); one-step workgroups
+  // keep the lean variant and its occupancy.
+  const bool pipe = p.split_tokens > W * CH;
+  const void* dk =
+      p.bt64 ? (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, true>)
+                     : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, false>))
+             : (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, true>)
+                     : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, false>));
+  const dim3 grid = p.plan_n > 0 ? dim3(p.plan_n, 1, 1) : dim3(p.max_splits, p.num_kv_heads, num_seqs);
   hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
   if (e != hipSuccess || p.decode_only) return e;
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
@@ -710,33 +764,66 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
 
 bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
 
-// Fill p.plan from host-side context lengths: every (sequence, split) of a
-// decode batch, longest sequences first, so the splits whose merge is
-// largest start streaming first and their merges overlap the rest of the
-// launch.  Returns the entry count, or 0 when the batch does not fit the
-// plan (the launch then uses the full (max_splits, Hkv, S) grid).
+// Fill p.plan from host-side context lengths: one entry per (sequence, kv
+// head, split) of a decode batch.  Workgroup x runs on XCD x % 8 (the
+// dispatcher's round-robin over XCDs), so the pairs are bin-packed onto the 8
+// XCDs by context length (longest first, each to the least loaded XCD) and a
+// pair's splits all get ids of one residue: its partials then meet in one L2.
+// Within an XCD the longest pairs come first, so their merges overlap the
+// streaming of shorter ones.  Returns the entry count (a multiple of 8,
+// unused slots kPlanEmpty), or 0 when the batch does not fit the plan (the
+// launch then uses the full (max_splits, Hkv, S) grid).
+int build_decode_plan_for(AttnParams& p, const std::vector<std::pair<int64_t, int>>& order, int split) {
+  constexpr int kXcds = 8;
+  int64_t units = 0;
+  for (const auto& pr : order) {
+    const int64_t n = (pr.first + split - 1) / split;
+    units += (n < 1 ? 1 : n) * p.num_kv_heads;
+  }
+  if (units > kPlanMax) return 0;
+  std::vector<uint32_t> bucket[kXcds];
+  int64_t load[kXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (const auto& [L, i] : order) {
+    int64_t n = (L + split - 1) / split;
+    n = n < 1 ? 1 : n;
+    for (int kvh = 0; kvh < p.num_kv_heads; ++kvh) {
+      int b = 0;
+      for (int x = 1; x < kXcds; ++x)
+        if (load[x] < load[b]) b = x;
+      load[b] += L + split / 4;  // tokens, plus a per-pair overhead
+      for (int64_t sp = 0; sp < n; ++sp)
+        bucket[b].push_back(static_cast<uint32_t>(i) | static_cast<uint32_t>(kvh) << 16 |
+                            static_cast<uint32_t>(sp) << 20 | static_cast<uint32_t>(n - 1) << 26);
+    }
+  }
+  size_t rows = 0;
+  for (int x = 0; x < kXcds; ++x) rows = bucket[x].size() > rows ? bucket[x].size() : rows;
+  if (rows * kXcds > static_cast<size_t>(kPlanMax)) return 0;
+  for (size_t k = 0; k < rows; ++k)
+    for (int x = 0; x < kXcds; ++x)
+      p.plan[k * kXcds + x] = k < bucket[x].size() ? bucket[x][k] : kPlanEmpty;
+  p.split_tokens = split;
+  return static_cast<int>(rows * kXcds);
+}
+
+// The split starts at the workspace layout's (so at most max_splits per
+// sequence) and doubles until the batch fits the plan: long contexts get
+// long splits, whose waves then pipeline their steps.
 int build_decode_plan(AttnParams& p, const void* lens, int lens64, int num_seqs) {
-  if (num_seqs > 0xFFFF || p.max_splits > 0xFF) return 0;
+  if (num_seqs > 0xFFFF || p.num_kv_heads > 16 || p.max_splits > 64) return 0;
   std::vector<std::pair<int64_t, int>> order(num_seqs);
-  int64_t total = 0;
   for (int i = 0; i < num_seqs; ++i) {
     int64_t L = lens64 ? static_cast<const int64_t*>(lens)[i] : static_cast<const int32_t*>(lens)[i];
     L = L < 0 ? 0 : (L < p.max_ctx ? L : p.max_ctx);
     order[i] = {L, i};
-    const int64_t n = (L + p.split_tokens - 1) / p.split_tokens;
-    total += n < 1 ? 1 : n;
   }
-  if (total > kPlanMax) return 0;
   std::stable_sort(order.begin(), order.end(),
                    [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a.first > b.first; });
-  int n_out = 0;
-  for (const auto& [L, i] : order) {
-    int64_t n = (L + p.split_tokens - 1) / p.split_tokens;
-    n = n < 1 ? 1 : n;
-    for (int64_t sp = 0; sp < n; ++sp)
-      p.plan[n_out++] = static_cast<uint32_t>(i) | static_cast<uint32_t>(sp) << 16 | static_cast<uint32_t>(n) << 24;
+  for (int64_t split = p.split_tokens;; split *= 2) {
+    const int n = build_decode_plan_for(p, order, static_cast<int>(split));
+    if (n > 0) return n;
+    if (split >= p.max_ctx || split > (1 << 24)) return 0;  // one split per sequence did not fit either
   }
-  return n_out;
 }
 
 }  // namespace

@@ -164,10 +164,21 @@ def test_decode_plan_and_full_grid_agree_bitwise():
     _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
+def test_decode_plan_long_splits_pipeline_steps():
+    """100 x ~2000 tokens do not fit the plan at 256-token splits; the plan
+    doubles the split until they do, and the waves then pipeline several steps."""
+    seqs = [2000 + 7 * i for i in range(100)]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=3)
+    got = _run(q, kc, vc, md, 0.125)
+    _assert_close(got, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+    nolist = make_md(seqs, [1] * len(seqs), tables, 16, with_cpu_lists=False)
+    _assert_close(_run(q, kc, vc, nolist, 0.125), got, torch.float16)
+
+
 def test_decode_plan_overflow_falls_back_to_full_grid():
-    """More (sequence, split) units than the plan holds: the full grid runs."""
-    seqs = [2000 + 7 * i for i in range(100)]  # 100 x 8 splits > 768 plan entries
-    q, kc, vc, md, _, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=3)
+    """More (sequence, kv head) pairs than the plan holds: the full grid runs."""
+    seqs = [37 + (7 * i) % 500 for i in range(400)]  # 800 pairs > 768 plan entries
+    q, kc, vc, md, _, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=4)
     _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
