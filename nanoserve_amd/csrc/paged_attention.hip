@@ -492,33 +492,36 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 }
 
 // --------------------------------------------------------------------------
-// Variable-length rows (prefill, chunked prefill, the prefill part of a mixed
-// batch): one workgroup per (sequence, kv head, block of 128 flattened
-// (query row, head) columns); K and V stream through LDS in 32-token stages
-// shared by the four waves.
+// Variable-length rows (prefill, chunked prefill, the prefill rows of a mixed
+// batch).  The columns of a (sequence, kv head) are its flattened (query row,
+// head of the group) pairs, ql * G of them; each wave owns CT 16-column tiles
+// and streams the pair's K/V itself from position 0 to the last key any of
+// its columns may see, CH tokens per step with the decode kernel's pipelined
+// loads (step i+1's K/V and step i+2's table entries in flight while step i
+// computes).  K stays in registers as the MFMA A operand; V goes through a
+// per-wave V^T tile in LDS.  The waves of a workgroup never synchronise; they
+// share K/V through L1/L2.
 // --------------------------------------------------------------------------
 template <int D>
-struct VarlenCfg {
-  static constexpr int KC = 32;                  // KV tokens per LDS stage
-  static constexpr int CT = 2;                   // 16-column tiles per wave
-  static constexpr int COLS = kWaves * CT * 16;  // columns per workgroup
-  static constexpr int NC = D / 32, NN = D / 16;
-  static constexpr int K_LD = D + 8;             // padded K row (elements)
-  static constexpr int VT_LD = KC + 4;           // padded V^T row (elements)
-  static constexpr int CHUNKS = KC * D / 8;      // 16-byte chunks per stage per tensor
-  static constexpr int CPT = CHUNKS / kThreads;  // per thread
-  static_assert(CHUNKS % kThreads == 0, "stage must split evenly over the workgroup");
+struct PrefillCfg {
+  static constexpr int W = kWaves;              // waves per workgroup
+  static constexpr int CT = 2;                  // 16-column tiles per wave
+  static constexpr int CH = D == 64 ? 64 : 32;  // tokens per wave per step (16 KiB of K+V)
+  static constexpr int NT = CH / 16, NC = D / 32, NN = D / 16;
+  static constexpr int VT_LD = CH + 4;
+  static constexpr int COLS = W * CT * 16;      // columns per workgroup
+  static constexpr int LDS = W * D * VT_LD * 2;
+  static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
 };
 
-template <class DT, int D>
+template <class DT, int D, class BTI>
 __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
-  using Cfg = VarlenCfg<D>;
+  using Cfg = PrefillCfg<D>;
   using T = typename DT::T;
   using V8 = typename DT::vec8;
-  constexpr int KC = Cfg::KC, CT = Cfg::CT, COLS = Cfg::COLS, NC = Cfg::NC, NN = Cfg::NN;
-  constexpr int K_LD = Cfg::K_LD, VT_LD = Cfg::VT_LD, CPT = Cfg::CPT;
-  __shared__ __attribute__((aligned(16))) T k_lds[KC * K_LD];
-  __shared__ __attribute__((aligned(16))) T vt_lds[D * VT_LD];
+  constexpr int CT = Cfg::CT, CH = Cfg::CH, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN;
+  constexpr int VT_LD = Cfg::VT_LD;
+  __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
 
   const int cb = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
@@ -529,19 +532,20 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
   if (ql <= 0 || (p.skip_decode_rows && ql == 1)) return;
   if (q0 < 0 || q0 + ql > p.num_tokens) return;
   const int64_t ncols = ql * G;
-  const int64_t c_begin = static_cast<int64_t>(cb) * COLS;
-  if (c_begin >= ncols) return;
+  const int64_t c_wave = static_cast<int64_t>(cb) * Cfg::COLS + w * CT * 16;  // this wave's first column
+  if (c_wave >= ncols) return;
   int64_t L = load_index(p.seq_lens, s, p.sl64);
   L = L < p.max_ctx ? L : p.max_ctx;
   const int64_t ctx0 = L - ql;  // absolute position of query row 0
   const int bs_mask = (1 << p.bs_shift) - 1;
 
+  // Q^T operands, causal limits and output rows of the wave's columns.
   V8 qop[CT][NC];
   int64_t qpos[CT], orow[CT];
   bool cval[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const int64_t c = c_begin + (w * CT + ct) * 16 + c16;
+    const int64_t c = c_wave + ct * 16 + c16;
     cval[ct] = c < ncols;
     const int64_t qi = cval[ct] ? c / G : 0;
     const int64_t h = cval[ct] ? c - qi * G : 0;
@@ -549,10 +553,13 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
     orow[ct] = ((q0 + qi) * p.num_heads + static_cast<int64_t>(kvh) * G + h) * D;
     const T* qrow = reinterpret_cast<const T*>(p.query) + orow[ct];
 #pragma unroll
-    for (int c = 0; c < NC; ++c)
-      qop[ct][c] = cval[ct] ? load16<DT>(qrow + 32 * c + 8 * g) : zero8<DT>();
+    for (int c2 = 0; c2 < NC; ++c2) qop[ct][c2] = load16<DT>(qrow + 32 * c2 + 8 * g);
+    if (!cval[ct])
+#pragma unroll
+      for (int c2 = 0; c2 < NC; ++c2) qop[ct][c2] = zero8<DT>();
   }
-  const int64_t c_last = (ncols < c_begin + COLS ? ncols : c_begin + COLS) - 1;
+  // Keys this wave needs: up to the causal limit of its last column.
+  const int64_t c_last = (ncols < c_wave + CT * 16 ? ncols : c_wave + CT * 16) - 1;
   int64_t kv_end = ctx0 + c_last / G + 1;
   kv_end = kv_end < L ? kv_end : L;
 
@@ -568,63 +575,86 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
   int bad = 0;
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
+  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
+  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
+  T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;
 
-  for (int64_t t0 = 0; t0 < kv_end; t0 += KC) {
-    u32x4 kraw[CPT], vraw[CPT];
+  auto table_step = [&](int64_t tb, int64_t (&bk)[NT]) {
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + i * kThreads;
-      const int tok = idx / (D / 8), ch = idx % (D / 8);
-      const int64_t t = t0 + tok;
+    for (int j = 0; j < NT; ++j) {
+      int64_t t = tb + 16 * j + c16;
+      t = t < kv_end ? t : kv_end - 1;
+      t = t > 0 ? t : 0;
+      bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+    }
+  };
+  auto issue_step = [&](int64_t tb, const int64_t (&bk)[NT], V8 (&kx)[NT][NC], V8 (&vx)[NT][NC]) {
+    int vmask = 0;
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int64_t t = tb + 16 * j + c16;
       bool valid = t < kv_end;
-      int64_t blk = 0;
-      if (valid) blk = load_index(p.bt, bt_row + (t >> p.bs_shift), p.bt64);
-      if (valid && (blk < 0 || blk >= p.num_blocks)) {
+      if (valid && (bk[j] < 0 || bk[j] >= p.num_blocks)) {
         bad = 1;
         valid = false;
       }
-      if (!valid) blk = 0;
-      const int64_t off = ((blk << p.bs_shift) + (t & bs_mask)) * slot_stride + static_cast<int64_t>(kvh) * D + ch * 8;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      kraw[i] = valid ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(p.k_cache) + off) : z;
-      vraw[i] = valid ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const T*>(p.v_cache) + off) : z;
-    }
-    __syncthreads();  // previous stage fully consumed
+      const int64_t off = valid ? ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const int idx = tid + i * kThreads;
-      const int tok = idx / (D / 8), ch = idx % (D / 8);
-      *reinterpret_cast<u32x4*>(k_lds + tok * K_LD + ch * 8) = kraw[i];
-      const V8 v8 = __builtin_bit_cast(V8, vraw[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) vt_lds[(ch * 8 + e) * VT_LD + tok] = v8[e];
+      for (int c2 = 0; c2 < NC; ++c2) {
+        kx[j][c2] = load16<DT>(kbase + off + 32 * c2);
+        vx[j][c2] = load16<DT>(vbase + off + 32 * c2);
+      }
+      vmask |= valid ? 1 << j : 0;
     }
-    __syncthreads();
+    return vmask;
+  };
 
-    V8 ka[2][NC];
+  int64_t blk[NT];
+  V8 kr[NT][NC], vr[NT][NC];
+  int vmask = 0;
+  if (kv_end > 0) {
+    table_step(0, blk);
+    vmask = issue_step(0, blk, kr, vr);
+    table_step(CH, blk);
+  }
+  for (int64_t tb = 0; tb < kv_end; tb += CH) {
+    const bool has_next = tb + CH < kv_end;
+    V8 kn[NT][NC], vn[NT][NC];
+    int vmask_n = 0;
+    if (has_next) {
+      vmask_n = issue_step(tb + CH, blk, kn, vn);
+      table_step(tb + 2 * CH, blk);
+    }
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NT; ++j)
+      if (!(vmask >> j & 1))
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
-        ka[j][c] = __builtin_bit_cast(V8, *reinterpret_cast<const u32x4*>(k_lds + (16 * j + c16) * K_LD + 32 * c + 8 * g));
-    V8 pt[CT];
+        for (int c2 = 0; c2 < NC; ++c2) vr[j][c2] = zero8<DT>();
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int c2 = 0; c2 < NC; ++c2)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vt[(32 * c2 + 8 * g + e) * VT_LD + 16 * j + c16] = vr[j][c2][e];
+
+    V8 pt[CT][NT / 2];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      floatx4 sacc[2];
+      floatx4 sacc[NT];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
+      for (int j = 0; j < NT; ++j) {
         sacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int c = 0; c < NC; ++c) sacc[j] = mfma16x16x32(DT{}, ka[j][c], qop[ct][c], sacc[j]);
+        for (int c2 = 0; c2 < NC; ++c2) sacc[j] = mfma16x16x32(DT{}, kr[j][c2], qop[ct][c2], sacc[j]);
       }
-      float sv[2][4];
+      float sv[NT][4];
       float mloc = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int64_t t = t0 + 16 * j + 4 * g + r;
-          const bool ok = cval[ct] && t <= qpos[ct] && t < L;
+          const int64_t t = tb + 16 * j + 4 * g + r;
+          const bool ok = cval[ct] && t <= qpos[ct] && t < kv_end;
           const float x = ok ? sacc[j][r] * p.scale_log2 : -INFINITY;
           sv[j][r] = x;
           mloc = fmaxf(mloc, x);
@@ -635,7 +665,7 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
       const float alpha = none ? 1.f : fast_exp2(m_run[ct] - m_new);
       float psum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < NT; ++j)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float pr = none ? 0.f : fast_exp2(sv[j][r] - m_new);
@@ -647,22 +677,38 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
       for (int n = 0; n < NN; ++n) acc[ct][n] *= alpha;
       m_run[ct] = m_new;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pt[ct][e] = static_cast<T>(sv[0][e]);
-        pt[ct][4 + e] = static_cast<T>(sv[1][e]);
-      }
+      for (int pb = 0; pb < NT / 2; ++pb)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pt[ct][pb][e] = static_cast<T>(sv[2 * pb][e]);
+          pt[ct][pb][4 + e] = static_cast<T>(sv[2 * pb + 1][e]);
+        }
     }
+    wave_lds_sync();
+    // O^T += V^T P^T; each V^T operand is read once and used by every column tile.
 #pragma unroll
-    for (int n = 0; n < NN; ++n) {
-      const T* r0 = vt_lds + (16 * n + c16) * VT_LD + 4 * g;
-      const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
-      const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
-      const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+    for (int pb = 0; pb < NT / 2; ++pb)
 #pragma unroll
-      for (int ct = 0; ct < CT; ++ct) acc[ct][n] = mfma16x16x32(DT{}, va, pt[ct], acc[ct][n]);
+      for (int n = 0; n < NN; ++n) {
+        const T* r0 = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
+        const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) acc[ct][n] = mfma16x16x32(DT{}, va, pt[ct][pb], acc[ct][n]);
+      }
+    wave_lds_sync();
+    if (has_next) {
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int c2 = 0; c2 < NC; ++c2) {
+          kr[j][c2] = kn[j][c2];
+          vr[j][c2] = vn[j][c2];
+        }
+      vmask = vmask_n;
     }
   }
-  bad = __syncthreads_or(bad);
 
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -755,9 +801,11 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
   if (e != hipSuccess || p.decode_only) return e;
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
-  const int64_t nblk = (cols + VarlenCfg<D>::COLS - 1) / VarlenCfg<D>::COLS;
+  const int64_t nblk = (cols + PrefillCfg<D>::COLS - 1) / PrefillCfg<D>::COLS;
   if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
-  return hipLaunchKernel(reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D>),
+  const void* vk = p.bt64 ? reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D, int64_t>)
+                          : reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D, int32_t>);
+  return hipLaunchKernel(vk,
                          dim3(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs),
                          dim3(kThreads), args, 0, stream);
 }
