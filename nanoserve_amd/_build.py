@@ -33,6 +33,9 @@ HIPCC_FLAGS = [
     "-shared",
     # Keep the compiler from forming packed-fp32 VALU instructions.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax rescales them every step, and
+    # AGPR accumulators would cost a read and a write per element each time.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
 ]
 

@@ -76,6 +76,37 @@ __device__ __forceinline__ float group4_sum(float v) {
   return v;
 }
 
+// The same reductions with gfx950's row-swap permutes (VALU, no LDS trip).
+// With both operands holding v, v_permlane16_swap leaves 16-lane rows
+// {0,0,2,2} of v in its first operand and {1,1,3,3} in its second, and
+// v_permlane32_swap halves {lo,lo} and {hi,hi}, so one max / add of the pair
+// is one butterfly stage.  They are written as asm: the compiler's builtin
+// for these swaps folds the second result into the first.
+__device__ __forceinline__ void swap_rows16(float& x, float& y) {
+  asm volatile("s_nop 4\n\tv_permlane16_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ void swap_halves32(float& x, float& y) {
+  asm volatile("s_nop 4\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+}
+__device__ __forceinline__ float group4_max_swap(float v) {
+  float x = v, y = v;
+  swap_rows16(x, y);
+  v = fmaxf(x, y);
+  x = v;
+  y = v;
+  swap_halves32(x, y);
+  return fmaxf(x, y);
+}
+__device__ __forceinline__ float group4_sum_swap(float v) {
+  float x = v, y = v;
+  swap_rows16(x, y);
+  v = x + y;
+  x = v;
+  y = v;
+  swap_halves32(x, y);
+  return x + y;
+}
+
 // LDS ordering between lanes of one wave: LDS instructions of a wave execute
 // in order, so a compiler-level fence is enough to make one lane's ds_write
 // visible to another lane's later ds_read.

@@ -493,55 +493,108 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 
 // --------------------------------------------------------------------------
 // Variable-length rows (prefill, chunked prefill, the prefill rows of a mixed
-// batch).  The columns of a (sequence, kv head) are its flattened (query row,
-// head of the group) pairs, ql * G of them; each wave owns CT 16-column tiles
-// and streams the pair's K/V itself from position 0 to the last key any of
-// its columns may see, CH tokens per step with the decode kernel's pipelined
-// loads (step i+1's K/V and step i+2's table entries in flight while step i
-// computes).  K stays in registers as the MFMA A operand; V goes through a
-// per-wave V^T tile in LDS.  The waves of a workgroup never synchronise; they
-// share K/V through L1/L2.
+// batch): flash-attention forward over the paged cache.  The columns of a
+// (sequence, kv head) are its flattened (query row, head of the group) pairs,
+// ql * G of them; a workgroup owns COLS of them (CT 16-column tiles per wave)
+// and walks the pair's keys from position 0 to the causal limit of its last
+// column, KT keys per step.  Each step's K and V tiles go from HBM straight
+// into LDS with global_load_lds (16 bytes per lane, no registers), two steps
+// ahead of the one being computed, through a ring of three LDS stages; the
+// four waves share every byte and one barrier per step hands a stage over.
+// The block-table entries of the keys come first into LDS (a window of TBL
+// entries), so the loads need no table round trip of their own.
+//
+// LDS layout of a stage: K tile then V tile, both [KT][D] rows of 16-byte
+// chunks, chunk c of key k stored at chunk c ^ k_swz(k) (K) or c ^ v_swz(k)
+// (V) of its row.  A DMA lane picks the global chunk that belongs at its LDS
+// slot, so the swizzle costs nothing on the write side and spreads the MFMA
+// operand reads (16-byte K rows, 2-byte V columns) over all banks.
 // --------------------------------------------------------------------------
-template <int D>
+template <int D, int CT_>
 struct PrefillCfg {
   static constexpr int W = kWaves;              // waves per workgroup
-  static constexpr int CT = 2;                  // 16-column tiles per wave
-  static constexpr int CH = D == 64 ? 64 : 32;  // tokens per wave per step (16 KiB of K+V)
-  static constexpr int NT = CH / 16, NC = D / 32, NN = D / 16;
-  static constexpr int VT_LD = CH + 4;
+  static constexpr int CT = CT_;                // 16-column tiles per wave
+  static constexpr int KT = 64;                 // keys per step
+  static constexpr int NT = KT / 16, NC = D / 32, NN = D / 16;
+  static constexpr int CPR = D / 8;             // 16-byte chunks per key row
+  static constexpr int TILE = KT * D * 2;       // bytes of one K or V tile
+  static constexpr int DMA = TILE / (kThreads * 16);  // 16-byte loads per thread per tile
+  static constexpr int NSTAGE = 3;
+  static constexpr int TBL = 4096;              // table entries per window
+  static constexpr int LDS = NSTAGE * 2 * TILE + TBL * 4 + 16;
   static constexpr int COLS = W * CT * 16;      // columns per workgroup
-  static constexpr int LDS = W * D * VT_LD * 2;
-  static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
+  static_assert(DMA >= 1 && DMA * kThreads * 16 == TILE, "loads must tile a K/V tile");
 };
 
-template <class DT, int D, class BTI>
-__global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
-  using Cfg = PrefillCfg<D>;
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// Address-space views for global_load_lds (global source, LDS destination).
+typedef __attribute__((address_space(1))) void* gbl_void_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+__device__ __forceinline__ int k_swz(int key) { return key & 7; }
+__device__ __forceinline__ int v_swz(int key) { return (key & 3) << 1; }
+
+// Wait until at most N of this wave's vector-memory operations are pending,
+// drain its LDS operations, then barrier.  Written as one asm statement so the
+// compiler adds no wait of its own for the LDS loads still in flight.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+  static_assert(N >= 0 && N <= 63, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+template <class DT, int D, int CT, class BTI>
+__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(AttnParams p) {
+  using Cfg = PrefillCfg<D, CT>;
   using T = typename DT::T;
   using V8 = typename DT::vec8;
-  constexpr int CT = Cfg::CT, CH = Cfg::CH, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN;
-  constexpr int VT_LD = Cfg::VT_LD;
+  constexpr int KT = Cfg::KT, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN;
+  constexpr int CPR = Cfg::CPR, TILE = Cfg::TILE, DMA = Cfg::DMA, W = Cfg::W;
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
+  int* tbl = reinterpret_cast<int*>(smem + Cfg::NSTAGE * 2 * TILE);
+  int* bad_first = tbl + Cfg::TBL;
 
   const int cb = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps step logic scalar
   const int G = p.group, Hkv = p.num_kv_heads;
 
+  // Positions are int32 (the host caps max_ctx below 2^31).
   const int64_t q0 = load_index(p.qsl, s, p.qsl64);
-  const int64_t ql = load_index(p.qsl, s + 1, p.qsl64) - q0;
-  if (ql <= 0 || (p.skip_decode_rows && ql == 1)) return;
-  if (q0 < 0 || q0 + ql > p.num_tokens) return;
-  const int64_t ncols = ql * G;
-  const int64_t c_wave = static_cast<int64_t>(cb) * Cfg::COLS + w * CT * 16;  // this wave's first column
-  if (c_wave >= ncols) return;
-  int64_t L = load_index(p.seq_lens, s, p.sl64);
-  L = L < p.max_ctx ? L : p.max_ctx;
-  const int64_t ctx0 = L - ql;  // absolute position of query row 0
-  const int bs_mask = (1 << p.bs_shift) - 1;
+  const int64_t ql64 = load_index(p.qsl, s + 1, p.qsl64) - q0;
+  if (ql64 <= 0 || (p.skip_decode_rows && ql64 == 1)) return;
+  if (q0 < 0 || q0 + ql64 > p.num_tokens) return;
+  const int64_t ncols = ql64 * G;
+  const int64_t c_wg = static_cast<int64_t>(cb) * Cfg::COLS;
+  if (c_wg >= ncols) return;
+  int64_t L64 = load_index(p.seq_lens, s, p.sl64);
+  L64 = L64 < p.max_ctx ? L64 : p.max_ctx;
+  const int L = static_cast<int>(L64 > 0 ? L64 : 0);
+  const int64_t ctx0 = L - ql64;  // absolute position of query row 0 (may be negative)
+  const int bs_shift = p.bs_shift;
+  const int bs_mask = (1 << bs_shift) - 1;
 
-  // Q^T operands, causal limits and output rows of the wave's columns.
+  // Keys the workgroup needs: up to the causal limit of its last column.
+  const int64_t c_last_wg = (ncols < c_wg + Cfg::COLS ? ncols : c_wg + Cfg::COLS) - 1;
+  int64_t kv_end64 = ctx0 + c_last_wg / G + 1;
+  kv_end64 = kv_end64 < L ? kv_end64 : L;
+  const int kv_end = static_cast<int>(kv_end64 > 0 ? kv_end64 : 0);
+
+  // This wave's columns: Q^T operands, causal limits, output rows.
+  const int64_t c_wave = c_wg + w * CT * 16;
+  const bool wave_on = c_wave < ncols;
+  int kv_end_w = 0;
+  int64_t qmin_w = -1;
+  if (wave_on) {
+    const int64_t c_last = (ncols < c_wave + CT * 16 ? ncols : c_wave + CT * 16) - 1;
+    const int64_t e = ctx0 + c_last / G + 1;
+    kv_end_w = static_cast<int>(e < 0 ? 0 : (e < L ? e : L));
+    qmin_w = ctx0 + c_wave / G;
+  }
   V8 qop[CT][NC];
-  int64_t qpos[CT], orow[CT];
+  int lim[CT];  // last key position a column may see (-1: none)
+  int64_t orow[CT];
   bool cval[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
@@ -549,19 +602,20 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
     cval[ct] = c < ncols;
     const int64_t qi = cval[ct] ? c / G : 0;
     const int64_t h = cval[ct] ? c - qi * G : 0;
-    qpos[ct] = ctx0 + qi;
+    const int64_t qpos = ctx0 + qi;
+    lim[ct] = cval[ct] ? static_cast<int>(qpos < kv_end_w - 1 ? qpos : kv_end_w - 1) : -1;
     orow[ct] = ((q0 + qi) * p.num_heads + static_cast<int64_t>(kvh) * G + h) * D;
     const T* qrow = reinterpret_cast<const T*>(p.query) + orow[ct];
 #pragma unroll
-    for (int c2 = 0; c2 < NC; ++c2) qop[ct][c2] = load16<DT>(qrow + 32 * c2 + 8 * g);
-    if (!cval[ct])
-#pragma unroll
-      for (int c2 = 0; c2 < NC; ++c2) qop[ct][c2] = zero8<DT>();
+    for (int c2 = 0; c2 < NC; ++c2) {
+      qop[ct][c2] = cval[ct] ? load16<DT>(qrow + 32 * c2 + 8 * g) : zero8<DT>();
+      // A negative scale moves into Q (exact sign flips), so the softmax can
+      // take maxima over raw scores and fold the scale into one FMA.
+      if (p.scale_log2 < 0.f)
+        qop[ct][c2] = __builtin_bit_cast(V8, __builtin_bit_cast(u32x4, qop[ct][c2]) ^ 0x80008000u);
+    }
   }
-  // Keys this wave needs: up to the causal limit of its last column.
-  const int64_t c_last = (ncols < c_wave + CT * 16 ? ncols : c_wave + CT * 16) - 1;
-  int64_t kv_end = ctx0 + c_last / G + 1;
-  kv_end = kv_end < L ? kv_end : L;
+  const float sc = fabsf(p.scale_log2);
 
   float m_run[CT], l_run[CT];
   floatx4 acc[CT][NN];
@@ -572,109 +626,109 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
 #pragma unroll
     for (int n = 0; n < NN; ++n) acc[ct][n] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
-  int bad = 0;
+
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
-  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
-  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
-  T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;
+  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D;
+  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D;
+  int e0 = 0;      // first table entry of the current window
+  int kv_win = 0;  // keys covered by the window's entries (and below kv_end)
 
-  auto table_step = [&](int64_t tb, int64_t (&bk)[NT]) {
+  // Start the K/V loads of `step` into `stage`.  Lane `lane` of load u of
+  // wave w fills 16-byte slot (u * W + w) * 64 + lane of each tile.  Keys
+  // past the window or kv_end read an in-bounds slot; their scores are
+  // masked and their V values replaced by zero when read.
+  auto dma = [&](int step, int stage) {
+    char* st = smem + stage * 2 * TILE;
 #pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      int64_t t = tb + 16 * j + c16;
-      t = t < kv_end ? t : kv_end - 1;
-      t = t > 0 ? t : 0;
-      bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+    for (int u = 0; u < DMA; ++u) {
+      const int pos = (u * W + w) * 64 + lane;
+      const int key = pos / CPR, pc = pos % CPR;
+      const int t = step * KT + key;
+      const bool in = t < kv_win;
+      const int blk = tbl[in ? (t >> bs_shift) - e0 : 0];
+      const bool valid = in && blk >= 0;
+      const int64_t off = valid ? ((static_cast<int64_t>(blk) << bs_shift) + (t & bs_mask)) * slot_stride : 0;
+      const T* gk = kbase + off + ((pc ^ k_swz(key)) << 3);
+      const T* gv = vbase + off + ((pc ^ v_swz(key)) << 3);
+      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gk), (lds_void_ptr)(st + (u * W + w) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gv), (lds_void_ptr)(st + TILE + (u * W + w) * 1024), 16, 0, 0);
     }
   };
-  auto issue_step = [&](int64_t tb, const int64_t (&bk)[NT], V8 (&kx)[NT][NC], V8 (&vx)[NT][NC]) {
-    int vmask = 0;
+
+  // One step of this wave's columns from `stage`.
+  auto compute = [&](int stage, int step) {
+    const int tb = step * KT;
+    if (tb >= kv_end_w) return;
+    const char* kt = smem + stage * 2 * TILE;
+    const char* vt = kt + TILE;
+    floatx4 sacc[CT][NT];
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
-      const int64_t t = tb + 16 * j + c16;
-      bool valid = t < kv_end;
-      if (valid && (bk[j] < 0 || bk[j] >= p.num_blocks)) {
-        bad = 1;
-        valid = false;
-      }
-      const int64_t off = valid ? ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
-#pragma unroll
-      for (int c2 = 0; c2 < NC; ++c2) {
-        kx[j][c2] = load16<DT>(kbase + off + 32 * c2);
-        vx[j][c2] = load16<DT>(vbase + off + 32 * c2);
-      }
-      vmask |= valid ? 1 << j : 0;
-    }
-    return vmask;
-  };
-
-  int64_t blk[NT];
-  V8 kr[NT][NC], vr[NT][NC];
-  int vmask = 0;
-  if (kv_end > 0) {
-    table_step(0, blk);
-    vmask = issue_step(0, blk, kr, vr);
-    table_step(CH, blk);
-  }
-  for (int64_t tb = 0; tb < kv_end; tb += CH) {
-    const bool has_next = tb + CH < kv_end;
-    V8 kn[NT][NC], vn[NT][NC];
-    int vmask_n = 0;
-    if (has_next) {
-      vmask_n = issue_step(tb + CH, blk, kn, vn);
-      table_step(tb + 2 * CH, blk);
-    }
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
-      if (!(vmask >> j & 1))
-#pragma unroll
-        for (int c2 = 0; c2 < NC; ++c2) vr[j][c2] = zero8<DT>();
-#pragma unroll
-    for (int j = 0; j < NT; ++j)
+      const int key = 16 * j + c16;
+      V8 kop[NC];
 #pragma unroll
       for (int c2 = 0; c2 < NC; ++c2)
+        kop[c2] = *reinterpret_cast<const V8*>(kt + key * D * 2 + (((4 * c2 + g) ^ k_swz(key)) << 4));
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(32 * c2 + 8 * g + e) * VT_LD + 16 * j + c16] = vr[j][c2][e];
-
+      for (int ct = 0; ct < CT; ++ct) {
+        sacc[ct][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c2 = 0; c2 < NC; ++c2) sacc[ct][j] = mfma16x16x32(DT{}, kop[c2], qop[ct][c2], sacc[ct][j]);
+      }
+    }
+    // Online softmax in base 2 (sc = |scale| * log2 e).  When every key of the
+    // step precedes every column of the wave, the maximum is taken over raw
+    // scores and p = exp2(s * sc - m) is one FMA; otherwise key
+    // tb + 16j + 4g + r of a column is masked by the column's limit.
+    const bool full = tb + KT - 1 <= qmin_w;
     V8 pt[CT][NT / 2];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
-      floatx4 sacc[NT];
-#pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        sacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int c2 = 0; c2 < NC; ++c2) sacc[j] = mfma16x16x32(DT{}, kr[j][c2], qop[ct][c2], sacc[j]);
-      }
       float sv[NT][4];
-      float mloc = -INFINITY;
+      float m_new, alpha;
+      if (full) {
+        float mloc = sacc[ct][0][0];
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+        for (int j = 0; j < NT; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t t = tb + 16 * j + 4 * g + r;
-          const bool ok = cval[ct] && t <= qpos[ct] && t < kv_end;
-          const float x = ok ? sacc[j][r] * p.scale_log2 : -INFINITY;
-          sv[j][r] = x;
-          mloc = fmaxf(mloc, x);
-        }
-      mloc = group4_max(mloc);
-      const float m_new = fmaxf(m_run[ct], mloc);
-      const bool none = m_new == -INFINITY;
-      const float alpha = none ? 1.f : fast_exp2(m_run[ct] - m_new);
+          for (int r = 0; r < 4; ++r) mloc = fmaxf(mloc, sacc[ct][j][r]);
+        m_new = fmaxf(m_run[ct], group4_max_swap(mloc) * sc);
+        alpha = fast_exp2(m_run[ct] - m_new);
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sv[j][r] = fast_exp2(__builtin_fmaf(sacc[ct][j][r], sc, -m_new));
+      } else {
+        const int room = lim[ct] - tb - 4 * g;
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sv[j][r] = 16 * j + r <= room ? sacc[ct][j][r] * sc : -INFINITY;
+            mloc = fmaxf(mloc, sv[j][r]);
+          }
+        m_new = fmaxf(m_run[ct], group4_max_swap(mloc));
+        const bool none = m_new == -INFINITY;
+        alpha = none ? 1.f : fast_exp2(m_run[ct] - m_new);
+        const float msub = none ? 0.f : m_new;  // exp2(-inf - 0) = 0 for fully masked columns
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sv[j][r] = fast_exp2(sv[j][r] - msub);
+      }
       float psum = 0.f;
 #pragma unroll
       for (int j = 0; j < NT; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float pr = none ? 0.f : fast_exp2(sv[j][r] - m_new);
-          sv[j][r] = pr;
-          psum += pr;
-        }
+        for (int r = 0; r < 4; ++r) psum += sv[j][r];
       l_run[ct] = l_run[ct] * alpha + psum;
+      // Rescale only when some column's maximum moved (alpha == 1 is exact).
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
-      for (int n = 0; n < NN; ++n) acc[ct][n] *= alpha;
+        for (int n = 0; n < NN; ++n) acc[ct][n] *= alpha;
+      }
       m_run[ct] = m_new;
 #pragma unroll
       for (int pb = 0; pb < NT / 2; ++pb)
@@ -684,37 +738,97 @@ __global__ __launch_bounds__(kThreads) void paged_varlen_kernel(AttnParams p) {
           pt[ct][pb][4 + e] = static_cast<T>(sv[2 * pb + 1][e]);
         }
     }
-    wave_lds_sync();
-    // O^T += V^T P^T; each V^T operand is read once and used by every column tile.
+    // O^T += V^T P^T.  k-slot 4h + e of lane group g is key 32pb + 16h + 4g + e,
+    // matching P^T.  ds_read_b64_tr_b16 gives lane i of a 16-lane group
+    // element e = element i & 3 of the 8 bytes lane (i >> 2) + 4e of the group
+    // addressed, so lane c16 of group g points at head dims 16n + 4 (c16 & 3)
+    // .. +3 of key 32pb + 16h + 4g + (c16 >> 2) and receives V^T row 16n + c16
+    // at keys 32pb + 16h + 4g + 0..3.  Keys at or past kv_end (only in the
+    // last step) contribute zero.
+    const bool vfull = tb + KT <= kv_end;
+    const int d0 = 4 * (c16 & 3);
 #pragma unroll
     for (int pb = 0; pb < NT / 2; ++pb)
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
-        const T* r0 = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
-        const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+        u32x2 half_op[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int key = 32 * pb + 16 * h + 4 * g + (c16 >> 2);
+          const int d = 16 * n + d0;
+          const char* src = vt + key * D * 2 + (((d >> 3) ^ v_swz(key)) << 4) + ((d & 7) << 1);
+          half_op[h] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                      (__attribute__((address_space(3))) short4_t*)(src)));
+        }
+        V8 va = __builtin_bit_cast(V8, u32x4{half_op[0][0], half_op[0][1], half_op[1][0], half_op[1][1]});
+        if (!vfull) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const int key = 32 * pb + 16 * (e >> 2) + 4 * g + (e & 3);
+            va[e] = tb + key < kv_end ? va[e] : static_cast<T>(0.f);
+          }
+        }
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[ct][n] = mfma16x16x32(DT{}, va, pt[ct][pb], acc[ct][n]);
       }
-    wave_lds_sync();
-    if (has_next) {
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int c2 = 0; c2 < NC; ++c2) {
-          kr[j][c2] = kn[j][c2];
-          vr[j][c2] = vn[j][c2];
-        }
-      vmask = vmask_n;
-    }
-  }
+  };
 
+  if (tid == 0) *bad_first = 0x7FFFFFFF;
+  const int nsteps = (kv_end + KT - 1) / KT;
+  const int nent = (kv_end + bs_mask) >> bs_shift;
+  const int win_steps = (Cfg::TBL << bs_shift) / KT;
+  for (int s0 = 0; s0 < nsteps; s0 += win_steps) {
+    const int s1 = s0 + win_steps < nsteps ? s0 + win_steps : nsteps;
+    e0 = (s0 * KT) >> bs_shift;
+    kv_win = s1 * KT < kv_end ? s1 * KT : kv_end;
+    const int ne = nent - e0 < Cfg::TBL ? nent - e0 : Cfg::TBL;
+    __syncthreads();  // the previous window's loads and table readers are done
+    for (int base = 0; base < ne; base += 4 * kThreads) {
+      int64_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        int i = base + u * kThreads + tid;
+        i = i < ne ? i : ne - 1;
+        v[u] = ld_idx<BTI>(p.bt, bt_row + e0 + i);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = base + u * kThreads + tid;
+        if (i < ne) {
+          const bool ok = v[u] >= 0 && v[u] < p.num_blocks;
+          tbl[i] = ok ? static_cast<int>(v[u]) : -1;
+          if (!ok) atomicMin(bad_first, e0 + i);
+        }
+      }
+    }
+    __syncthreads();
+
+    // Steps s0 .. s1-1 through the three stages: at the top of step i the
+    // loads of step i+1 may still be in flight (2 * DMA per thread), step i's
+    // have landed once every wave has waited for its own and passed the
+    // barrier; then step i+2's loads go into the stage step i-1 used.  Steps
+    // past s1 still load (nothing valid) so the pending count stays exact.
+    dma(s0, 0);
+    dma(s0 + 1, 1);
+    int stage = 0;
+    for (int i = s0; i < s1; ++i) {
+      stage_barrier<2 * DMA>();
+      dma(i + 2, stage == 0 ? 2 : stage - 1);
+      compute(stage, i);
+      stage = stage == 2 ? 0 : stage + 1;
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  __syncthreads();
+  const int need_w = (kv_end_w + bs_mask) >> bs_shift;
+  const bool bad_w = *bad_first < need_w;
+
+  if (!wave_on) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
-    const float lsum = group4_sum(l_run[ct]);
+    const float lsum = group4_sum_swap(l_run[ct]);
     if (!cval[ct]) continue;
-    const float inv = bad ? NAN : (lsum > 0.f ? 1.f / lsum : 0.f);
+    const float inv = bad_w ? NAN : (lsum > 0.f ? 1.f / lsum : 0.f);
     T* orow_p = reinterpret_cast<T*>(p.out) + orow[ct];
 #pragma unroll
     for (int n = 0; n < NN; ++n) {
@@ -782,6 +896,9 @@ int64_t round_up_ctx(int max_seq_len, int block_size) {
   return (static_cast<int64_t>(max_seq_len) + block_size - 1) / block_size * block_size;
 }
 
+// 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
+constexpr int kPrefillTiles = 2;
+
 template <class DT, int D>
 hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipStream_t stream) {
   void* args[] = {&p};
@@ -801,10 +918,11 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
   if (e != hipSuccess || p.decode_only) return e;
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
-  const int64_t nblk = (cols + PrefillCfg<D>::COLS - 1) / PrefillCfg<D>::COLS;
+  using PCfg = PrefillCfg<D, kPrefillTiles>;
+  const int64_t nblk = (cols + PCfg::COLS - 1) / PCfg::COLS;
   if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const void* vk = p.bt64 ? reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D, int64_t>)
-                          : reinterpret_cast<const void*>(&paged_varlen_kernel<DT, D, int32_t>);
+  const void* vk = p.bt64 ? reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int64_t>)
+                          : reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int32_t>);
   return hipLaunchKernel(vk,
                          dim3(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs),
                          dim3(kThreads), args, 0, stream);
@@ -926,6 +1044,9 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads) return NS_ERR_INVALID_ARG;
   if (num_blocks <= 0 || block_table_width <= 0 || block_table_stride < block_table_width)
     return NS_ERR_INVALID_ARG;
+  // The prefill kernel keeps block ids and key positions as 32-bit values.
+  if (!is_decode_only && num_blocks > 0x7FFFFFFF) return NS_ERR_UNSUPPORTED;
+  if (!is_decode_only && static_cast<int64_t>(max_seq_len) + block_size > 0x7FFFFFFF) return NS_ERR_UNSUPPORTED;
   if (max_seq_len < 0 || max_query_len < 0) return NS_ERR_INVALID_ARG;
   if (!(scale == scale)) return NS_ERR_INVALID_ARG;
   const int bs_shift = ilog2_exact(block_size);

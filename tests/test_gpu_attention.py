@@ -273,6 +273,27 @@ def test_prefill_head_shapes(D, group):
     _assert_close(_run(q, kc, vc, md, scale), paged_attention_ref(q, kc, vc, md, scale), torch.float16)
 
 
+@pytest.mark.parametrize("seqs,qls", [([9000, 300], [5, 40]), ([4200, 70], [150, 70])])
+def test_prefill_block_size_one_crosses_table_windows(seqs, qls):
+    """Block size 1 makes one table entry per key, so a workgroup's keys span
+    several 4096-entry table windows (the second case puts a window edge
+    inside the causal band of the chunk)."""
+    q, kc, vc, md, _, _ = _case(seqs, qls, 14, 2, 64, 1, torch.float16)
+    _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+
+
+def test_prefill_invalid_block_id_poisons_only_its_sequence():
+    seqs = [300, 64]
+    kc, vc, tables, _ = build_paged(seqs, 32, 16, 2, 64, dtype=torch.float16)
+    md = make_md(seqs, seqs, tables, 16)
+    md.block_tables[0, 0] = 10_000  # every row of sequence 0 needs block 0
+    q = torch.randn(sum(seqs), 14, 64).half()
+    got = _run(q, kc, vc, md, 0.125)
+    assert torch.isnan(got[:300]).all()
+    md_ok = make_md(seqs, seqs, tables, 16)
+    _assert_close(got[300:], paged_attention_ref(q, kc, vc, md_ok, 0.125)[300:], torch.float16)
+
+
 def test_chunked_prefill_matches_whole_prefill():
     sl = 200
     q, kc, vc, md, tables, _ = _case([sl], [sl], 14, 2, 64, 16, torch.float16)
