@@ -108,14 +108,14 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  *
  * seq_lens_host (optional, may be NULL) is a HOST copy of seq_lens -- the
  * reference's AttentionMetadata.seq_lens_cpu (attention.py:52-54), which its
- * non-decode path already treats as authoritative (attention.py:124).  For a
- * decode-only batch it lets the library launch exactly one workgroup per
+ * non-decode path already treats as authoritative (attention.py:124).  It
+ * lets the library launch the decode rows as exactly one workgroup per
  * (sequence, kv head, context split), longest sequences first, instead of a
  * grid sized by max_seq_len.  It must equal seq_lens; a device length longer
- * than the host copy makes that sequence's outputs NaN.
+ * than the host copy makes that decode row's outputs NaN.
  *
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
- * Supported: head_dim in {64, 128}; block_size a power of two in [8, 256];
+ * Supported: head_dim in {64, 128}; block_size a power of two;
  * num_heads / num_kv_heads <= 16.  Loops are bounded by each sequence's
  * length (never by the block-table width), so zero-padded table rows are
  * safe.  A block id outside [0, num_blocks) is never dereferenced; the

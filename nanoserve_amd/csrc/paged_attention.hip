@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -27,8 +28,6 @@
 namespace ns {
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * 64;
 // Plan entries carried in the kernel arguments (keeps them under 4 KiB).
 constexpr int kPlanMax = 768;
 constexpr uint32_t kPlanEmpty = 0xFFFFFFFFu;  // plan slot with no work (sequence ids stay below 0xFFFF)
@@ -495,35 +494,48 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 // Variable-length rows (prefill, chunked prefill, the prefill rows of a mixed
 // batch): flash-attention forward over the paged cache.  The columns of a
 // (sequence, kv head) are its flattened (query row, head of the group) pairs,
-// ql * G of them; a workgroup owns COLS of them (CT 16-column tiles per wave)
-// and walks the pair's keys from position 0 to the causal limit of its last
-// column, KT keys per step.  Each step's K and V tiles go from HBM straight
-// into LDS with global_load_lds (16 bytes per lane, no registers), two steps
-// ahead of the one being computed, through a ring of three LDS stages; the
-// four waves share every byte and one barrier per step hands a stage over.
-// The block-table entries of the keys come first into LDS (a window of TBL
-// entries), so the loads need no table round trip of their own.
+// ql * G of them; a workgroup owns COLS of them and walks the pair's keys
+// from position 0 to the causal limit of its last column, KT keys per step.
+//
+// The workgroup is KG key groups of WC waves.  Wave i of every group owns the
+// same CT 16-column tiles; group k takes steps k, k + KG, k + 2KG, ... with
+// its own running (max, sum, O) and the groups are merged through LDS at the
+// end, so the dependent chain of steps is KG times shorter and each SIMD
+// holds KG waves.  Each step's K and V tiles go from HBM straight into LDS
+// with global_load_lds (16 bytes per lane, no registers), two macro-steps
+// (KG steps each) ahead of the one being computed, through a ring of three
+// macro-slots; every byte is read once per workgroup and one barrier per
+// macro-step hands a slot over.  The block-table entries of the keys come
+// first into LDS (a window of TBL entries), so the loads need no table round
+// trip of their own.
 //
 // LDS layout of a stage: K tile then V tile, both [KT][D] rows of 16-byte
 // chunks, chunk c of key k stored at chunk c ^ k_swz(k) (K) or c ^ v_swz(k)
 // (V) of its row.  A DMA lane picks the global chunk that belongs at its LDS
 // slot, so the swizzle costs nothing on the write side and spreads the MFMA
-// operand reads (16-byte K rows, 2-byte V columns) over all banks.
+// operand reads (16-byte K rows; 8-byte transposing V reads) over all banks.
 // --------------------------------------------------------------------------
 template <int D, int CT_>
 struct PrefillCfg {
-  static constexpr int W = kWaves;              // waves per workgroup
+  static constexpr int KG = 2;                  // key groups
+  static constexpr int WC = 4;                  // column waves per group
+  static constexpr int W = KG * WC;             // waves per workgroup
+  static constexpr int THREADS = W * 64;
   static constexpr int CT = CT_;                // 16-column tiles per wave
-  static constexpr int KT = 64;                 // keys per step
+  static constexpr int KT = D == 64 ? 64 : 32;  // keys per step (8 KiB per tile)
   static constexpr int NT = KT / 16, NC = D / 32, NN = D / 16;
   static constexpr int CPR = D / 8;             // 16-byte chunks per key row
   static constexpr int TILE = KT * D * 2;       // bytes of one K or V tile
-  static constexpr int DMA = TILE / (kThreads * 16);  // 16-byte loads per thread per tile
-  static constexpr int NSTAGE = 3;
+  static constexpr int DMA = TILE / (THREADS * 16);  // 16-byte loads per thread per tile
+  static constexpr int NSLOT = 3;               // macro-slots in the ring
+  static constexpr int RING = NSLOT * KG * 2 * TILE;
   static constexpr int TBL = 4096;              // table entries per window
-  static constexpr int LDS = NSTAGE * 2 * TILE + TBL * 4 + 16;
-  static constexpr int COLS = W * CT * 16;      // columns per workgroup
-  static_assert(DMA >= 1 && DMA * kThreads * 16 == TILE, "loads must tile a K/V tile");
+  static constexpr int LDS = RING + TBL * 4 + 16;
+  static constexpr int COLS = WC * CT * 16;     // columns per workgroup
+  static constexpr int NF = CT * (NN * 4 + 2);  // floats per lane a group hands over in the merge
+  static_assert(DMA >= 1 && DMA * THREADS * 16 == TILE, "loads must tile a K/V tile");
+  static_assert(NT % 2 == 0, "P^T operand pairs two 16-key tiles");
+  static_assert(WC * NF * 64 * 4 <= RING, "merge buffer fits the ring");
 };
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -544,20 +556,24 @@ __device__ __forceinline__ void stage_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+constexpr int kPrefillThreads = 512;
+
 template <class DT, int D, int CT, class BTI>
-__global__ __launch_bounds__(kThreads) void paged_prefill_kernel(AttnParams p) {
+__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnParams p) {
   using Cfg = PrefillCfg<D, CT>;
+  static_assert(Cfg::THREADS == kPrefillThreads, "launch bounds match the workgroup");
   using T = typename DT::T;
   using V8 = typename DT::vec8;
-  constexpr int KT = Cfg::KT, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN;
+  constexpr int KT = Cfg::KT, NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, KG = Cfg::KG;
   constexpr int CPR = Cfg::CPR, TILE = Cfg::TILE, DMA = Cfg::DMA, W = Cfg::W;
   __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
-  int* tbl = reinterpret_cast<int*>(smem + Cfg::NSTAGE * 2 * TILE);
+  int* tbl = reinterpret_cast<int*>(smem + Cfg::RING);
   int* bad_first = tbl + Cfg::TBL;
 
   const int cb = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps step logic scalar
+  const int kg = w / Cfg::WC, wc = w % Cfg::WC;            // key group, column wave
   const int G = p.group, Hkv = p.num_kv_heads;
 
   // Positions are int32 (the host caps max_ctx below 2^31).
@@ -582,7 +598,7 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(AttnParams p) {
   const int kv_end = static_cast<int>(kv_end64 > 0 ? kv_end64 : 0);
 
   // This wave's columns: Q^T operands, causal limits, output rows.
-  const int64_t c_wave = c_wg + w * CT * 16;
+  const int64_t c_wave = c_wg + wc * CT * 16;
   const bool wave_on = c_wave < ncols;
   int kv_end_w = 0;
   int64_t qmin_w = -1;
@@ -774,26 +790,32 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(AttnParams p) {
   };
 
   if (tid == 0) *bad_first = 0x7FFFFFFF;
-  const int nsteps = (kv_end + KT - 1) / KT;
+  // Macro-step M covers steps M * KG + k, k < KG (step M * KG + k by group k).
+  constexpr int MKEYS = KG * KT;
+  const int nmacro = (kv_end + MKEYS - 1) / MKEYS;
   const int nent = (kv_end + bs_mask) >> bs_shift;
-  const int win_steps = (Cfg::TBL << bs_shift) / KT;
-  for (int s0 = 0; s0 < nsteps; s0 += win_steps) {
-    const int s1 = s0 + win_steps < nsteps ? s0 + win_steps : nsteps;
-    e0 = (s0 * KT) >> bs_shift;
-    kv_win = s1 * KT < kv_end ? s1 * KT : kv_end;
+  const int win_macro = (Cfg::TBL << bs_shift) / MKEYS;
+  auto dma_macro = [&](int M, int slot) {
+#pragma unroll
+    for (int k = 0; k < KG; ++k) dma(M * KG + k, slot * KG + k);
+  };
+  for (int M0 = 0; M0 < nmacro; M0 += win_macro) {
+    const int M1 = M0 + win_macro < nmacro ? M0 + win_macro : nmacro;
+    e0 = (M0 * MKEYS) >> bs_shift;
+    kv_win = M1 * MKEYS < kv_end ? M1 * MKEYS : kv_end;
     const int ne = nent - e0 < Cfg::TBL ? nent - e0 : Cfg::TBL;
     __syncthreads();  // the previous window's loads and table readers are done
-    for (int base = 0; base < ne; base += 4 * kThreads) {
+    for (int base = 0; base < ne; base += 4 * Cfg::THREADS) {
       int64_t v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        int i = base + u * kThreads + tid;
+        int i = base + u * Cfg::THREADS + tid;
         i = i < ne ? i : ne - 1;
         v[u] = ld_idx<BTI>(p.bt, bt_row + e0 + i);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int i = base + u * kThreads + tid;
+        const int i = base + u * Cfg::THREADS + tid;
         if (i < ne) {
           const bool ok = v[u] >= 0 && v[u] < p.num_blocks;
           tbl[i] = ok ? static_cast<int>(v[u]) : -1;
@@ -803,27 +825,64 @@ __global__ __launch_bounds__(kThreads) void paged_prefill_kernel(AttnParams p) {
     }
     __syncthreads();
 
-    // Steps s0 .. s1-1 through the three stages: at the top of step i the
-    // loads of step i+1 may still be in flight (2 * DMA per thread), step i's
+    // Macro-steps M0 .. M1-1 through the three slots: at the top of macro-step
+    // M the loads of M+1 may still be in flight (KG * 2 * DMA per thread), M's
     // have landed once every wave has waited for its own and passed the
-    // barrier; then step i+2's loads go into the stage step i-1 used.  Steps
-    // past s1 still load (nothing valid) so the pending count stays exact.
-    dma(s0, 0);
-    dma(s0 + 1, 1);
-    int stage = 0;
-    for (int i = s0; i < s1; ++i) {
-      stage_barrier<2 * DMA>();
-      dma(i + 2, stage == 0 ? 2 : stage - 1);
-      compute(stage, i);
-      stage = stage == 2 ? 0 : stage + 1;
+    // barrier; then M+2's loads go into the slot M-1 used.  Macro-steps past
+    // M1 still load (nothing valid) so the pending count stays exact.
+    dma_macro(M0, 0);
+    dma_macro(M0 + 1, 1);
+    int slot = 0;
+    for (int M = M0; M < M1; ++M) {
+      stage_barrier<KG * 2 * DMA>();
+      dma_macro(M + 2, slot == 0 ? 2 : slot - 1);
+      compute(slot * KG + kg, M * KG + kg);
+      slot = slot == 2 ? 0 : slot + 1;
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
-  __syncthreads();
+  __syncthreads();  // every group's steps are done; the ring is free
   const int need_w = (kv_end_w + bs_mask) >> bs_shift;
   const bool bad_w = *bad_first < need_w;
 
-  if (!wave_on) return;
+  // Merge the key groups into group 0 through LDS, [wave][float][lane].
+  float* mbuf = reinterpret_cast<float*>(smem) + wc * Cfg::NF * 64 + lane;
+#pragma unroll
+  for (int k = 1; k < KG; ++k) {
+    if (kg == k && wave_on) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        mbuf[(ct * (NN * 4 + 2)) * 64] = m_run[ct];
+        mbuf[(ct * (NN * 4 + 2) + 1) * 64] = l_run[ct];
+#pragma unroll
+        for (int n = 0; n < NN; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) mbuf[(ct * (NN * 4 + 2) + 2 + 4 * n + r) * 64] = acc[ct][n][r];
+      }
+    }
+    __syncthreads();
+    if (kg == 0 && wave_on) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const float mo = mbuf[(ct * (NN * 4 + 2)) * 64];
+        const float lo = mbuf[(ct * (NN * 4 + 2) + 1) * 64];
+        const float m = fmaxf(m_run[ct], mo);
+        const bool none = m == -INFINITY;
+        const float a0 = none ? 0.f : fast_exp2(m_run[ct] - m);
+        const float a1 = none ? 0.f : fast_exp2(mo - m);
+        l_run[ct] = l_run[ct] * a0 + lo * a1;
+        m_run[ct] = m;
+#pragma unroll
+        for (int n = 0; n < NN; ++n)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            acc[ct][n][r] = acc[ct][n][r] * a0 + mbuf[(ct * (NN * 4 + 2) + 2 + 4 * n + r) * 64] * a1;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (kg != 0 || !wave_on) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float lsum = group4_sum_swap(l_run[ct]);
@@ -899,6 +958,44 @@ int64_t round_up_ctx(int max_seq_len, int block_size) {
 // 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
 constexpr int kPrefillTiles = 2;
 
+// A mixed batch runs its decode rows on a side stream, forked from and joined
+// back to the caller's stream with events, so the memory-bound decode kernel
+// overlaps the compute-bound prefill kernel.  One side stream (default
+// priority) and event pair per device, created on first use outside graph
+// capture; the fork/join is an ordinary cross-stream dependency, which graph
+// capture records as such.  Without them the two launches run in order on
+// the caller's stream.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool failed = false;
+};
+constexpr int kMaxDevices = 64;
+std::mutex g_side_mu;
+SideStream g_side[kMaxDevices];
+
+SideStream* side_stream_for(hipStream_t st) {
+  int dev = -1, sdev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  if (st != nullptr && (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev)) return nullptr;
+  SideStream& ss = g_side[dev];
+  if (ss.stream) return &ss;
+  if (ss.failed) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess) ss.stream = nullptr;
+  if (ss.stream && hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess) ss.fork = nullptr;
+  if (ss.fork && hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) ss.join = nullptr;
+  if (!ss.join) {
+    if (ss.fork) (void)hipEventDestroy(ss.fork);
+    if (ss.stream) (void)hipStreamDestroy(ss.stream);
+    ss = SideStream{};
+    ss.failed = true;
+    return nullptr;
+  }
+  return &ss;
+}
+
 template <class DT, int D>
 hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipStream_t stream) {
   void* args[] = {&p};
@@ -915,17 +1012,33 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
              : (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, true>)
                      : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, false>));
   const dim3 grid = p.plan_n > 0 ? dim3(p.plan_n, 1, 1) : dim3(p.max_splits, p.num_kv_heads, num_seqs);
-  hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
-  if (e != hipSuccess || p.decode_only) return e;
+  if (p.decode_only) return hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
+
   const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
   using PCfg = PrefillCfg<D, kPrefillTiles>;
   const int64_t nblk = (cols + PCfg::COLS - 1) / PCfg::COLS;
   if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
   const void* vk = p.bt64 ? reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int64_t>)
                           : reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int32_t>);
-  return hipLaunchKernel(vk,
-                         dim3(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs),
-                         dim3(kThreads), args, 0, stream);
+  const dim3 vgrid(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs);
+
+  std::lock_guard<std::mutex> lock(g_side_mu);
+  SideStream* ss = side_stream_for(stream);
+  if (!ss) {
+    hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
+    if (e != hipSuccess) return e;
+    return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), args, 0, stream);
+  }
+  hipError_t e = hipEventRecord(ss->fork, stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(ss->stream, ss->fork, 0);
+  if (e != hipSuccess) return e;
+  // Once the side stream depends on the caller's, it is joined back whatever
+  // else fails (an unjoined fork would also break a graph capture).
+  const hipError_t ed = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, ss->stream);
+  const hipError_t er = hipEventRecord(ss->join, ss->stream);
+  const hipError_t ev = hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), args, 0, stream);
+  const hipError_t ej = er == hipSuccess ? hipStreamWaitEvent(stream, ss->join, 0) : er;
+  return ed != hipSuccess ? ed : (ev != hipSuccess ? ev : ej);
 }
 
 bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
@@ -1098,7 +1211,10 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   p.part_ml_bytes = static_cast<int>(wl.o_off - wl.ml_off);
   p.part_o_bytes = static_cast<int>(wl.total - wl.o_off);
   p.plan_n = 0;
-  if (seq_lens_host && is_decode_only)
+  // The plan covers every sequence; in a mixed batch the workgroups of
+  // sequences with more than one query row leave at once (the prefill kernel
+  // owns them).
+  if (seq_lens_host)
     p.plan_n = build_decode_plan(p, seq_lens_host, seq_lens_host_is_int64, num_seqs);
 
   hipStream_t st = static_cast<hipStream_t>(stream);

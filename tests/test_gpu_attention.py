@@ -350,13 +350,16 @@ def test_repeated_calls_reuse_workspace():
         assert torch.equal(o, outs[0])
 
 
-def test_graph_replays_match_eager():
-    """Capture decode calls in a HIP graph; every replay matches the eager result.
+@pytest.mark.parametrize("config", ["c2", "c3"])
+def test_graph_replays_match_eager(config):
+    """Capture calls in a HIP graph; every replay matches the eager result.
 
     Eager calls run between replays, so the split-K counters a replay leaves
-    behind are exercised by the eager path and the other way round.
+    behind are exercised by the eager path and the other way round.  The mixed
+    c3 batch forks its decode rows onto the library's side stream, so its
+    capture records the fork and the join.
     """
-    case = make_case("c2", seed=5, device=DEV, gen_device=DEV)
+    case = make_case(config, seed=5, device=DEV, gen_device=DEV)
     eager = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale).clone()
     torch.cuda.synchronize()
     s = torch.cuda.Stream()
