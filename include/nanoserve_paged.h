@@ -78,11 +78,15 @@ int ns_reshape_and_cache(const void* key, const void* value,
 /*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
  * ns_paged_attention needs for these sizes (split-K partials and counters).
+ * Without is_decode_only it includes the prefill split state: a fixed 512
+ * slots of 40 KiB (head_dim 64) or 72 KiB (head_dim 128).
  *
  * The workspace must be zero-filled once when it is first allocated; every
- * call leaves its counters at zero again, so the same buffer can be reused by
- * later calls on the same stream without clearing.  Calls that overlap in
- * time (different streams) must use different workspaces.
+ * call leaves its counters at zero again, and the counters sit at the same
+ * offsets for every call (a fixed 4 MiB head of the workspace), so the same
+ * buffer can be reused by later calls of any shape on the same stream
+ * without clearing.  Calls that overlap in time (different streams) must use
+ * different workspaces.
  */
 size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
                                          int head_dim, int block_size,
@@ -114,6 +118,16 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  * grid sized by max_seq_len.  It must equal seq_lens; a device length longer
  * than the host copy makes that decode row's outputs NaN.
  *
+ * query_start_loc_host (optional, may be NULL; read only with seq_lens_host
+ * and without is_decode_only) is a HOST copy of query_start_loc -- the
+ * reference's AttentionMetadata.query_start_loc_cpu (attention.py:53-54).
+ * With it the prefill rows are scheduled exactly: heaviest column blocks
+ * first, long key ranges split across workgroups and merged in-launch (the
+ * workspace holds the split state), and the decode launch is skipped when no
+ * sequence has a single query row.  It must equal query_start_loc; a
+ * sequence whose device query length differs has its reached outputs
+ * written as NaN (nothing is read or written out of bounds).
+ *
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
  * Supported: head_dim in {64, 128}; block_size a power of two;
  * num_heads / num_kv_heads <= 16.  Loops are bounded by each sequence's
@@ -128,6 +142,7 @@ int ns_paged_attention(void* out, const void* query,
                        const void* seq_lens, int seq_lens_is_int64,
                        const void* query_start_loc, int query_start_loc_is_int64,
                        const void* seq_lens_host, int seq_lens_host_is_int64,
+                       const void* query_start_loc_host, int query_start_loc_host_is_int64,
                        int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
                        int is_decode_only,
                        int num_heads, int num_kv_heads, int head_dim,

@@ -57,6 +57,7 @@ SIGNATURES = {
         c_void_p, c_int,                         # seq_lens, is_int64
         c_void_p, c_int,                         # query_start_loc, is_int64
         c_void_p, c_int,                         # seq_lens_host (host memory, optional), is_int64
+        c_void_p, c_int,                         # query_start_loc_host (host memory, optional), is_int64
         c_int, c_int64, c_int, c_int, c_int,     # S, T, max_query_len, max_seq_len, decode_only
         c_int, c_int, c_int, c_int, c_int64,     # Hq, Hkv, D, block_size, num_blocks
         c_float, c_int,                          # scale, dtype

@@ -139,13 +139,19 @@ def paged_attention_hip(
         qsl = _index(md.query_start_loc, "query_start_loc", device).contiguous()
         qsl_ptr, qsl64 = qsl.data_ptr(), int(qsl.dtype == torch.int64)
 
-    # The host copy of the lengths lets the library size the decode grid
-    # exactly (one workgroup per split, longest sequences first).
+    # The host copies of the lengths and query offsets let the library size
+    # its grids exactly: one decode workgroup per split (longest sequences
+    # first), and prefill key ranges split across the CUs.
     lens_host = None
     if md.seq_lens_cpu is not None:
         if len(md.seq_lens_cpu) < md.num_seqs:
             raise ValueError("seq_lens_cpu is shorter than num_seqs")
         lens_host = (ctypes.c_int64 * md.num_seqs)(*md.seq_lens_cpu[:md.num_seqs])
+    qsl_host = None
+    if not decode_only and md.query_start_loc_cpu is not None:
+        if len(md.query_start_loc_cpu) < md.num_seqs + 1:
+            raise ValueError("query_start_loc_cpu is shorter than num_seqs + 1")
+        qsl_host = (ctypes.c_int64 * (md.num_seqs + 1))(*md.query_start_loc_cpu[:md.num_seqs + 1])
 
     stream = torch.cuda.current_stream(device).cuda_stream
     nbytes = lib.ns_paged_attention_workspace_size(
@@ -163,6 +169,7 @@ def paged_attention_hip(
         sl.data_ptr(), int(sl.dtype == torch.int64),
         qsl_ptr, qsl64,
         lens_host, 1,
+        qsl_host, 1,
         md.num_seqs, num_tokens, md.max_query_len, md.max_seq_len, int(decode_only),
         num_heads, num_kv_heads, head_dim, block_size, num_blocks,
         float(scale), _lib.DTYPE_CODES[q.dtype],

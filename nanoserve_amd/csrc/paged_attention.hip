@@ -56,9 +56,17 @@ struct AttnParams {
   float* part_ml;         // [S, Hkv, max_splits, G, 2]  (running max, running sum)
   int part_o_bytes, part_ml_bytes;
   unsigned* counters;     // [S, Hkv] arrivals per (sequence, kv head); left at zero
-  int plan_n;             // decode workgroups listed in plan (0: no plan)
+  // Prefill split-K: partial slots of one workgroup's columns each, and one
+  // arrival counter per split (sequence, kv head, column block); left at zero.
+  float* pf_part;
+  int pf_part_bytes;
+  unsigned* pf_counters;
+  int plan_n;             // decode: workgroups listed in plan; prefill: sequences listed (0: no plan)
   // Decode schedule from host-side lengths: entry x = s | kvh << 16 | split << 20 |
   // (nsplit - 1) << 26 for workgroup x, or kPlanEmpty.
+  // Prefill schedule (its own copy of the parameters): two entries per listed
+  // sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
+  // slot_base | pair_base << 16.
   uint32_t plan[kPlanMax];
 };
 
@@ -533,6 +541,8 @@ struct PrefillCfg {
   static constexpr int LDS = RING + TBL * 4 + 16;
   static constexpr int COLS = WC * CT * 16;     // columns per workgroup
   static constexpr int NF = CT * (NN * 4 + 2);  // floats per lane a group hands over in the merge
+  static constexpr int PU = CT * (NN + 1);      // 16-byte units per lane of a split's partial
+  static constexpr int SLOT_BYTES = WC * PU * 64 * 16;
   static_assert(DMA >= 1 && DMA * THREADS * 16 == TILE, "loads must tile a K/V tile");
   static_assert(NT % 2 == 0, "P^T operand pairs two 16-key tiles");
   static_assert(WC * NF * 64 * 4 <= RING, "merge buffer fits the ring");
@@ -570,11 +580,29 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
   int* tbl = reinterpret_cast<int*>(smem + Cfg::RING);
   int* bad_first = tbl + Cfg::TBL;
 
-  const int cb = blockIdx.x, kvh = blockIdx.y, s = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps step logic scalar
   const int kg = w / Cfg::WC, wc = w % Cfg::WC;            // key group, column wave
   const int G = p.group, Hkv = p.num_kv_heads;
+
+  // Work item: (sequence, kv head, column block) and, with a plan, the split
+  // of its key range.  Planned items run the heaviest column blocks first.
+  int s, kvh, split = 0, nsplit = 1, split_mk = 0, slot_base = 0, pair_base = 0;
+  int64_t ql_host = -1;
+  if (p.plan_n > 0) {
+    const uint32_t e0w = p.plan[3 * blockIdx.y], e1w = p.plan[3 * blockIdx.y + 1];
+    ql_host = p.plan[3 * blockIdx.y + 2];
+    s = static_cast<int>(e0w & 0xFFFFu);
+    nsplit = static_cast<int>((e0w >> 16) & 0x3Fu) + 1;
+    split_mk = static_cast<int>(e0w >> 22);
+    slot_base = static_cast<int>(e1w & 0xFFFFu);
+    pair_base = static_cast<int>(e1w >> 16);
+    kvh = static_cast<int>(blockIdx.x % Hkv);
+    split = static_cast<int>((blockIdx.x / Hkv) % nsplit);
+  } else {
+    kvh = blockIdx.y;
+    s = blockIdx.z;
+  }
 
   // Positions are int32 (the host caps max_ctx below 2^31).
   const int64_t q0 = load_index(p.qsl, s, p.qsl64);
@@ -582,7 +610,23 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
   if (ql64 <= 0 || (p.skip_decode_rows && ql64 == 1)) return;
   if (q0 < 0 || q0 + ql64 > p.num_tokens) return;
   const int64_t ncols = ql64 * G;
-  const int64_t c_wg = static_cast<int64_t>(cb) * Cfg::COLS;
+  const int64_t ncb = (ncols + Cfg::COLS - 1) / Cfg::COLS;
+  int64_t cb = blockIdx.x;
+  bool plan_broken = false;
+  if (p.plan_n > 0) {
+    const int64_t rcb = blockIdx.x / Hkv / nsplit;
+    if (rcb >= ncb) return;
+    cb = ncb - 1 - rcb;
+    // A device query length the host plan did not describe is a broken
+    // contract: the blocks it reaches are written as NaN and no split state
+    // (slots, counters) is touched.
+    if (ql64 != ql_host) {
+      if (split != 0) return;
+      plan_broken = true;
+      nsplit = 1;
+    }
+  }
+  const int64_t c_wg = cb * Cfg::COLS;
   if (c_wg >= ncols) return;
   int64_t L64 = load_index(p.seq_lens, s, p.sl64);
   L64 = L64 < p.max_ctx ? L64 : p.max_ctx;
@@ -791,19 +835,27 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
 
   if (tid == 0) *bad_first = 0x7FFFFFFF;
   // Macro-step M covers steps M * KG + k, k < KG (step M * KG + k by group k).
+  // A split runs macro-steps [M_begin, M_end) of the column block's range.
   constexpr int MKEYS = KG * KT;
   const int nmacro = (kv_end + MKEYS - 1) / MKEYS;
-  const int nent = (kv_end + bs_mask) >> bs_shift;
+  int nsplit_eff = 1, M_begin = 0, M_end = nmacro;
+  if (nsplit > 1) {
+    nsplit_eff = nmacro > split_mk ? (nmacro + split_mk - 1) / split_mk : 1;
+    if (split >= nsplit_eff) return;  // no keys for this split: it does not arrive
+    M_begin = split * split_mk;
+    M_end = M_begin + split_mk < nmacro ? M_begin + split_mk : nmacro;
+  }
   const int win_macro = (Cfg::TBL << bs_shift) / MKEYS;
   auto dma_macro = [&](int M, int slot) {
 #pragma unroll
     for (int k = 0; k < KG; ++k) dma(M * KG + k, slot * KG + k);
   };
-  for (int M0 = 0; M0 < nmacro; M0 += win_macro) {
-    const int M1 = M0 + win_macro < nmacro ? M0 + win_macro : nmacro;
+  for (int M0 = M_begin; M0 < M_end; M0 += win_macro) {
+    const int M1 = M0 + win_macro < M_end ? M0 + win_macro : M_end;
     e0 = (M0 * MKEYS) >> bs_shift;
     kv_win = M1 * MKEYS < kv_end ? M1 * MKEYS : kv_end;
-    const int ne = nent - e0 < Cfg::TBL ? nent - e0 : Cfg::TBL;
+    const int ne_all = ((kv_win + bs_mask) >> bs_shift) - e0;
+    const int ne = ne_all < Cfg::TBL ? ne_all : Cfg::TBL;
     __syncthreads();  // the previous window's loads and table readers are done
     for (int base = 0; base < ne; base += 4 * Cfg::THREADS) {
       int64_t v[4];
@@ -882,12 +934,92 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
     __syncthreads();
   }
 
+  bool bad_out = bad_w || plan_broken;
+  if (nsplit_eff > 1) {
+    // Split-K: park this split's state in its slot ([wave][float][lane], a
+    // bad table entry as l = NaN), count the arrival, and let the last split
+    // of the column block merge all slots in split order.
+    const int pair = pair_base + static_cast<int>(kvh * ncb + cb);
+    const int slot0 = slot_base + (kvh * static_cast<int>(ncb) + static_cast<int>(cb)) * nsplit;
+    const __amdgpu_buffer_rsrc_t pr =
+        __builtin_amdgcn_make_buffer_rsrc(p.pf_part, static_cast<short>(0), p.pf_part_bytes, kBufferWord3);
+    // Slot layout [wave][ct][unit][lane] of 16-byte units: unit 0 is
+    // (m, l, 0, 0), unit 1 + n is O^T tile n.  Units are stored whole (b128)
+    // and read as runs of b32 loads, which the backend merges: storing single
+    // vector elements with buffer stores miscompiles with ROCm 7.2's clang.
+    auto uofs = [&](int sl, int ct, int u) {
+      return sl * Cfg::SLOT_BYTES + (((wc * CT + ct) * (NN + 1) + u) * 64 + lane) * 16;
+    };
+    if (kg == 0 && wave_on) {
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        const float lw = bad_out ? NAN : l_run[ct];
+        __builtin_amdgcn_raw_buffer_store_b128(
+            u32x4{__builtin_bit_cast(uint32_t, m_run[ct]), __builtin_bit_cast(uint32_t, lw), 0u, 0u}, pr,
+            uofs(slot0 + split, ct, 0), 0, kSc1);
+#pragma unroll
+        for (int n = 0; n < NN; ++n)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[ct][n]), pr,
+                                                 uofs(slot0 + split, ct, 1 + n), 0, kSc1);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are acknowledged
+    __syncthreads();
+    int* s_last = bad_first;  // the table window is done with it
+    if (tid == 0) {
+      const unsigned prev = __hip_atomic_fetch_add(&p.pf_counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *s_last = prev == static_cast<unsigned>(nsplit_eff - 1);
+    }
+    __syncthreads();
+    if (!*s_last) return;
+    if (kg == 0 && wave_on) {
+      // Two passes over the slots, each with its loads independent of one
+      // another: the common maximum, then the rescaled sums in split order.
+      bad_out = false;
+      float mx[CT];
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) mx[ct] = -INFINITY;
+#pragma unroll 8
+      for (int k = 0; k < nsplit_eff; ++k)
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) mx[ct] = fmaxf(mx[ct], ld_sc1(pr, uofs(slot0 + k, ct, 0)));
+#pragma unroll
+      for (int ct = 0; ct < CT; ++ct) {
+        m_run[ct] = mx[ct];
+        l_run[ct] = 0.f;
+#pragma unroll
+        for (int n = 0; n < NN; ++n) acc[ct][n] = floatx4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll 2
+      for (int k = 0; k < nsplit_eff; ++k) {
+#pragma unroll
+        for (int ct = 0; ct < CT; ++ct) {
+          const int o0 = uofs(slot0 + k, ct, 0);
+          const float mk = ld_sc1(pr, o0);
+          const float lk = ld_sc1(pr, o0 + 4);
+          floatx4 ak[NN];
+#pragma unroll
+          for (int n = 0; n < NN; ++n) {
+            const int on = uofs(slot0 + k, ct, 1 + n);
+            ak[n] = floatx4{ld_sc1(pr, on), ld_sc1(pr, on + 4), ld_sc1(pr, on + 8), ld_sc1(pr, on + 12)};
+          }
+          bad_out |= lk != lk;
+          const float a = mx[ct] == -INFINITY ? 0.f : fast_exp2(mk - mx[ct]);
+          l_run[ct] += lk * a;
+#pragma unroll
+          for (int n = 0; n < NN; ++n) acc[ct][n] += ak[n] * a;
+        }
+      }
+    }
+    if (tid == 0) __hip_atomic_store(&p.pf_counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
   if (kg != 0 || !wave_on) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float lsum = group4_sum_swap(l_run[ct]);
     if (!cval[ct]) continue;
-    const float inv = bad_w ? NAN : (lsum > 0.f ? 1.f / lsum : 0.f);
+    const float inv = bad_out ? NAN : (lsum > 0.f ? 1.f / lsum : 0.f);
     T* orow_p = reinterpret_cast<T*>(p.out) + orow[ct];
 #pragma unroll
     for (int n = 0; n < NN; ++n) {
@@ -906,6 +1038,9 @@ struct DecodePlan {
   int split_tokens;
   int max_splits;
 };
+
+// 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
+constexpr int kPrefillTiles = 2;
 
 // Decode launch shape: kDecodeWaves waves per workgroup, each moving
 // decode_chunk<D> tokens (16 KiB of K+V) per step.
@@ -927,20 +1062,39 @@ DecodePlan plan_decode(int head_dim, int64_t ctx_tokens) {
 }
 
 struct WorkspaceLayout {
-  size_t counters_off, ml_off, o_off, total;
+  size_t counters_off, ml_off, o_off;
+  size_t pf_counters_off, pf_part_off, pf_part_bytes;  // prefill split-K region (0 bytes: none)
+  size_t total;
 };
+
+// Prefill split-K slots a workspace provides (one per split of a column
+// block), and the bytes of one slot: a workgroup's per-lane softmax state.
+constexpr int kPrefillSlots = 512;
+size_t prefill_slot_bytes(int head_dim) {
+  return head_dim == 64 ? PrefillCfg<64, kPrefillTiles>::SLOT_BYTES : PrefillCfg<128, kPrefillTiles>::SLOT_BYTES;
+}
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// Arrival counters sit at the same offsets for every call (decode pairs from
+// 0, prefill pairs after kMaxDecodePairs), ahead of all partials: a workspace
+// reused by calls of other shapes never has one call's partials where another
+// call's counters are, so the counters stay at zero between calls.
+constexpr size_t kMaxDecodePairs = (size_t{1} << 20) - kPrefillSlots;
+constexpr size_t kCounterBytes = (kMaxDecodePairs + kPrefillSlots) * sizeof(unsigned);
+
 WorkspaceLayout workspace_layout(int num_seqs, int num_kv_heads, int group, int head_dim,
-                                 const DecodePlan& plan) {
+                                 const DecodePlan& plan, bool with_prefill) {
   const size_t pairs = static_cast<size_t>(num_seqs) * num_kv_heads;
   const size_t parts = pairs * plan.max_splits * group;
   WorkspaceLayout l;
   l.counters_off = 0;
-  l.ml_off = align_up(pairs * sizeof(unsigned), 256);
+  l.pf_counters_off = kMaxDecodePairs * sizeof(unsigned);
+  l.ml_off = kCounterBytes;
   l.o_off = align_up(l.ml_off + parts * 2 * sizeof(float), 256);
-  l.total = align_up(l.o_off + parts * head_dim * sizeof(float), 256);
+  l.pf_part_off = align_up(l.o_off + parts * head_dim * sizeof(float), 256);
+  l.pf_part_bytes = with_prefill ? kPrefillSlots * prefill_slot_bytes(head_dim) : 0;
+  l.total = align_up(l.pf_part_off + l.pf_part_bytes, 256);
   return l;
 }
 
@@ -955,8 +1109,6 @@ int64_t round_up_ctx(int max_seq_len, int block_size) {
   return (static_cast<int64_t>(max_seq_len) + block_size - 1) / block_size * block_size;
 }
 
-// 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
-constexpr int kPrefillTiles = 2;
 
 // A mixed batch runs its decode rows on a side stream, forked from and joined
 // back to the caller's stream with events, so the memory-bound decode kernel
@@ -996,9 +1148,14 @@ SideStream* side_stream_for(hipStream_t st) {
   return &ss;
 }
 
+// Launch the decode kernel with `p` and, unless the batch is decode-only,
+// the prefill kernel with `pp` (its own plan); `launch_decode` is false when
+// the host query offsets show no one-row sequence.
 template <class DT, int D>
-hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipStream_t stream) {
+hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool launch_decode, int num_seqs,
+                            int max_query_len, hipStream_t stream) {
   void* args[] = {&p};
+  void* pargs[] = {&pp};
   constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
   // The block-table width is a template argument so table loads need no
   // per-lane branch.
@@ -1014,20 +1171,26 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   const dim3 grid = p.plan_n > 0 ? dim3(p.plan_n, 1, 1) : dim3(p.max_splits, p.num_kv_heads, num_seqs);
   if (p.decode_only) return hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
 
-  const int64_t cols = static_cast<int64_t>(max_query_len) * p.group;
   using PCfg = PrefillCfg<D, kPrefillTiles>;
-  const int64_t nblk = (cols + PCfg::COLS - 1) / PCfg::COLS;
-  if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
-  const void* vk = p.bt64 ? reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int64_t>)
-                          : reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int32_t>);
-  const dim3 vgrid(static_cast<unsigned>(nblk), p.num_kv_heads, num_seqs);
+  const void* vk = pp.bt64 ? reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int64_t>)
+                           : reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int32_t>);
+  dim3 vgrid;
+  if (pp.plan_n > 0) {
+    vgrid = dim3(static_cast<unsigned>(pf_grid_x), static_cast<unsigned>(pp.plan_n), 1);
+  } else {
+    const int64_t cols = static_cast<int64_t>(max_query_len) * pp.group;
+    const int64_t nblk = (cols + PCfg::COLS - 1) / PCfg::COLS;
+    if (nblk > 0x7FFFFFFF) return hipErrorInvalidValue;
+    vgrid = dim3(static_cast<unsigned>(nblk), pp.num_kv_heads, num_seqs);
+  }
+  if (!launch_decode) return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
 
   std::lock_guard<std::mutex> lock(g_side_mu);
   SideStream* ss = side_stream_for(stream);
   if (!ss) {
     hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
     if (e != hipSuccess) return e;
-    return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), args, 0, stream);
+    return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
   }
   hipError_t e = hipEventRecord(ss->fork, stream);
   if (e == hipSuccess) e = hipStreamWaitEvent(ss->stream, ss->fork, 0);
@@ -1036,7 +1199,7 @@ hipError_t launch_attention(AttnParams& p, int num_seqs, int max_query_len, hipS
   // else fails (an unjoined fork would also break a graph capture).
   const hipError_t ed = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, ss->stream);
   const hipError_t er = hipEventRecord(ss->join, ss->stream);
-  const hipError_t ev = hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), args, 0, stream);
+  const hipError_t ev = hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
   const hipError_t ej = er == hipSuccess ? hipStreamWaitEvent(stream, ss->join, 0) : er;
   return ed != hipSuccess ? ed : (ev != hipSuccess ? ev : ej);
 }
@@ -1088,20 +1251,111 @@ int build_decode_plan_for(AttnParams& p, const std::vector<std::pair<int64_t, in
 // The split starts at the workspace layout's (so at most max_splits per
 // sequence) and doubles until the batch fits the plan: long contexts get
 // long splits, whose waves then pipeline their steps.
-int build_decode_plan(AttnParams& p, const void* lens, int lens64, int num_seqs) {
+int64_t host_index(const void* a, int is64, int64_t i) {
+  return is64 ? static_cast<const int64_t*>(a)[i] : static_cast<const int32_t*>(a)[i];
+}
+
+// With host query offsets only the one-row sequences are planned (a batch
+// without any gets an empty plan, -1, and no decode launch).
+int build_decode_plan(AttnParams& p, const void* lens, int lens64, const void* qsl, int qsl64, int num_seqs) {
   if (num_seqs > 0xFFFF || p.num_kv_heads > 16 || p.max_splits > 64) return 0;
-  std::vector<std::pair<int64_t, int>> order(num_seqs);
+  std::vector<std::pair<int64_t, int>> order;
+  order.reserve(num_seqs);
   for (int i = 0; i < num_seqs; ++i) {
-    int64_t L = lens64 ? static_cast<const int64_t*>(lens)[i] : static_cast<const int32_t*>(lens)[i];
+    if (qsl && host_index(qsl, qsl64, i + 1) - host_index(qsl, qsl64, i) != 1) continue;
+    int64_t L = host_index(lens, lens64, i);
     L = L < 0 ? 0 : (L < p.max_ctx ? L : p.max_ctx);
-    order[i] = {L, i};
+    order.push_back({L, i});
   }
+  if (order.empty()) return -1;
   std::stable_sort(order.begin(), order.end(),
                    [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a.first > b.first; });
   for (int64_t split = p.split_tokens;; split *= 2) {
     const int n = build_decode_plan_for(p, order, static_cast<int>(split));
     if (n > 0) return n;
     if (split >= p.max_ctx || split > (1 << 24)) return 0;  // one split per sequence did not fit either
+  }
+}
+
+// Fill pp.plan with the prefill schedule from host query offsets and lengths:
+// every sequence with more than one query row, heaviest first, three entries
+// each (s | (nsplit - 1) << 16 | split_macro << 22; slot_base | pair_base << 16;
+// ql).  A column block's key range is cut into splits of split_macro
+// macro-steps so that no workgroup carries more than about twice an even
+// share of the batch's work over the 256 CUs (a long context behind a short
+// chunk); splits need partial slots, so the share doubles until the slots
+// fit.  Returns the sequences listed (0: no plan, the launch then uses the
+// full grid without splits) and the grid width.
+int build_prefill_plan(AttnParams& pp, const void* lens, int lens64, const void* qsl, int qsl64, int num_seqs,
+                       int cols_per_wg, int macro_keys, int& grid_x) {
+  constexpr int kCUs = 256, kMinSplitMacro = 4, kMaxListed = kPlanMax / 3;
+  struct Seq {
+    int s, ncb;
+    int64_t ql, nm_max, work;
+  };
+  std::vector<Seq> seqs;
+  int64_t total = 0;
+  for (int i = 0; i < num_seqs; ++i) {
+    const int64_t ql = host_index(qsl, qsl64, i + 1) - host_index(qsl, qsl64, i);
+    if (ql <= 1) continue;
+    int64_t L = host_index(lens, lens64, i);
+    L = L < 0 ? 0 : (L < pp.max_ctx ? L : pp.max_ctx);
+    const int64_t ncols = ql * pp.group;
+    const int64_t ncb = (ncols + cols_per_wg - 1) / cols_per_wg;
+    if (ncb > 0x7FFF) return 0;
+    Seq q{i, static_cast<int>(ncb), ql, 0, 0};
+    for (int64_t cb = 0; cb < ncb; ++cb) {
+      const int64_t c_last = (ncols < (cb + 1) * cols_per_wg ? ncols : (cb + 1) * cols_per_wg) - 1;
+      int64_t kv_end = L - ql + c_last / pp.group + 1;
+      kv_end = kv_end < 0 ? 0 : (kv_end < L ? kv_end : L);
+      const int64_t nm = (kv_end + macro_keys - 1) / macro_keys;
+      q.work += nm * pp.num_kv_heads;
+      q.nm_max = nm > q.nm_max ? nm : q.nm_max;
+    }
+    total += q.work;
+    seqs.push_back(q);
+  }
+  if (seqs.empty() || static_cast<int>(seqs.size()) > kMaxListed) return 0;
+  std::stable_sort(seqs.begin(), seqs.end(), [](const Seq& a, const Seq& b) { return a.nm_max > b.nm_max; });
+  // A workgroup holds a whole CU, so once the column blocks alone fill the
+  // CUs, splits only add merges: split what is longer than twice the even
+  // share.
+  int64_t share = 2 * ((total + kCUs - 1) / kCUs);
+  share = share < kMinSplitMacro ? kMinSplitMacro : share;
+  for (;; share *= 2) {
+    int64_t slots = 0, pairs = 0, gx = 0;
+    bool fits = true;
+    for (size_t k = 0; k < seqs.size(); ++k) {
+      const Seq& q = seqs[k];
+      int64_t nsplit = (q.nm_max + share - 1) / share;
+      nsplit = nsplit < 1 ? 1 : (nsplit > 64 ? 64 : nsplit);
+      int64_t split_mk = (q.nm_max + nsplit - 1) / nsplit;
+      if (split_mk > 1023) {
+        nsplit = 1;
+        split_mk = 0;
+      }
+      const int64_t items = static_cast<int64_t>(pp.num_kv_heads) * q.ncb * nsplit;
+      if (nsplit > 1) {
+        if (slots + items > kPrefillSlots || slots > 0xFFFF || pairs > 0xFFFF) {
+          fits = false;
+          break;
+        }
+      }
+      pp.plan[3 * k] = static_cast<uint32_t>(q.s) | static_cast<uint32_t>(nsplit - 1) << 16 |
+                       static_cast<uint32_t>(split_mk) << 22;
+      pp.plan[3 * k + 1] = static_cast<uint32_t>(slots) | static_cast<uint32_t>(pairs) << 16;
+      pp.plan[3 * k + 2] = static_cast<uint32_t>(q.ql);
+      if (nsplit > 1) {
+        slots += items;
+        pairs += static_cast<int64_t>(pp.num_kv_heads) * q.ncb;
+      }
+      gx = items > gx ? items : gx;
+    }
+    if (fits) {
+      if (gx > 0x7FFFFFFF) return 0;
+      grid_x = static_cast<int>(gx);
+      return static_cast<int>(seqs.size());
+    }
   }
 }
 
@@ -1119,7 +1373,7 @@ extern "C" const char* ns_error_string(int code) {
   }
 }
 
-extern "C" int ns_version(void) { return 100; }
+extern "C" int ns_version(void) { return 200; }
 
 extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
                                                     int head_dim, int block_size,
@@ -1127,12 +1381,12 @@ extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads,
                                                     int64_t num_tokens, int is_decode_only) {
   (void)max_query_len;
   (void)num_tokens;
-  (void)is_decode_only;
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads ||
       block_size <= 0 || max_seq_len < 0 || (head_dim != 64 && head_dim != 128))
     return 0;
   const ns::DecodePlan plan = ns::plan_decode(head_dim, ns::round_up_ctx(max_seq_len, block_size));
-  return ns::workspace_layout(num_seqs, num_kv_heads, num_heads / num_kv_heads, head_dim, plan).total;
+  return ns::workspace_layout(num_seqs, num_kv_heads, num_heads / num_kv_heads, head_dim, plan, !is_decode_only)
+      .total;
 }
 
 extern "C" int ns_paged_attention(void* out, const void* query,
@@ -1142,6 +1396,7 @@ extern "C" int ns_paged_attention(void* out, const void* query,
                                   const void* seq_lens, int seq_lens_is_int64,
                                   const void* query_start_loc, int query_start_loc_is_int64,
                                   const void* seq_lens_host, int seq_lens_host_is_int64,
+                                  const void* query_start_loc_host, int query_start_loc_host_is_int64,
                                   int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
                                   int is_decode_only,
                                   int num_heads, int num_kv_heads, int head_dim,
@@ -1174,10 +1429,11 @@ extern "C" int ns_paged_attention(void* out, const void* query,
 
   const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
   const DecodePlan plan = plan_decode(head_dim, ctx_plan);
-  const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan);
+  const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan, !is_decode_only);
   if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
   // Partials are addressed through buffer descriptors with 32-bit offsets.
-  if (wl.total - wl.o_off > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
+  if (wl.pf_part_off - wl.o_off > 0x7FFFFFFFu || wl.pf_part_bytes > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
+  if (static_cast<size_t>(num_seqs) * num_kv_heads > kMaxDecodePairs) return NS_ERR_UNSUPPORTED;
 
   AttnParams p;
   p.out = static_cast<char*>(out);
@@ -1209,21 +1465,44 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   p.part_ml = reinterpret_cast<float*>(ws + wl.ml_off);
   p.part_o = reinterpret_cast<float*>(ws + wl.o_off);
   p.part_ml_bytes = static_cast<int>(wl.o_off - wl.ml_off);
-  p.part_o_bytes = static_cast<int>(wl.total - wl.o_off);
+  p.part_o_bytes = static_cast<int>(wl.pf_part_off - wl.o_off);
+  p.pf_counters = reinterpret_cast<unsigned*>(ws + wl.pf_counters_off);
+  p.pf_part = reinterpret_cast<float*>(ws + wl.pf_part_off);
+  p.pf_part_bytes = static_cast<int>(wl.pf_part_bytes);
   p.plan_n = 0;
-  // The plan covers every sequence; in a mixed batch the workgroups of
-  // sequences with more than one query row leave at once (the prefill kernel
-  // owns them).
-  if (seq_lens_host)
-    p.plan_n = build_decode_plan(p, seq_lens_host, seq_lens_host_is_int64, num_seqs);
+  // Decode plan from the host lengths.  Without host query offsets a mixed
+  // batch's plan covers every sequence and the workgroups of sequences with
+  // more than one query row leave at once (the prefill kernel owns them).
+  const void* qsl_host = is_decode_only ? nullptr : query_start_loc_host;
+  bool launch_decode = true;
+  if (seq_lens_host) {
+    const int n = build_decode_plan(p, seq_lens_host, seq_lens_host_is_int64, qsl_host,
+                                    query_start_loc_host_is_int64, num_seqs);
+    launch_decode = n >= 0;
+    p.plan_n = n > 0 ? n : 0;
+  }
+  // Prefill plan (split-K over the CUs) from host offsets and lengths.
+  AttnParams pp;
+  int pf_grid_x = 0;
+  if (!is_decode_only) {
+    pp = p;
+    pp.plan_n = 0;
+    if (seq_lens_host && qsl_host) {
+      const int mkeys = head_dim == 64 ? PrefillCfg<64, kPrefillTiles>::KG * PrefillCfg<64, kPrefillTiles>::KT
+                                       : PrefillCfg<128, kPrefillTiles>::KG * PrefillCfg<128, kPrefillTiles>::KT;
+      pp.plan_n = build_prefill_plan(pp, seq_lens_host, seq_lens_host_is_int64, qsl_host,
+                                     query_start_loc_host_is_int64, num_seqs, PrefillCfg<64, kPrefillTiles>::COLS,
+                                     mkeys, pf_grid_x);
+    }
+  }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (dtype == NS_DTYPE_F16)
-    e = head_dim == 64 ? launch_attention<F16, 64>(p, num_seqs, max_query_len, st)
-                       : launch_attention<F16, 128>(p, num_seqs, max_query_len, st);
+    e = head_dim == 64 ? launch_attention<F16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st)
+                       : launch_attention<F16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st);
   else
-    e = head_dim == 64 ? launch_attention<BF16, 64>(p, num_seqs, max_query_len, st)
-                       : launch_attention<BF16, 128>(p, num_seqs, max_query_len, st);
+    e = head_dim == 64 ? launch_attention<BF16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st)
+                       : launch_attention<BF16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }

@@ -282,6 +282,30 @@ def test_prefill_block_size_one_crosses_table_windows(seqs, qls):
     _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
+@pytest.mark.parametrize("D,dtype", [(64, torch.float16), (128, torch.bfloat16)])
+def test_prefill_long_context_splits_match_unsplit(D, dtype):
+    """With host offsets the long key ranges of a chunked prefill are split
+    across workgroups and merged in-launch; without them every column block
+    walks its whole range.  Both match the oracle."""
+    seqs, qls = [4000, 900, 35], [300, 900, 1]
+    q, kc, vc, md, tables, _ = _case(seqs, qls, 14, 2, D, 16, dtype)
+    md_plain = make_md(seqs, qls, tables, 16, with_cpu_lists=False)
+    ref = paged_attention_ref(q, kc, vc, md, 0.125)
+    _assert_close(_run(q, kc, vc, md, 0.125), ref, dtype, "planned")
+    _assert_close(_run(q, kc, vc, md_plain, 0.125), ref, dtype, "unplanned")
+
+
+def test_prefill_host_offsets_that_disagree_poison_only_their_sequence():
+    seqs, qls = [3000, 64], [200, 64]
+    q, kc, vc, md, _, _ = _case(seqs, qls, 14, 2, 64, 16, torch.float16)
+    ref = paged_attention_ref(q, kc, vc, md, 0.125)
+    md.query_lens_cpu = [100, 64]
+    md.query_start_loc_cpu = [0, 100, 164]  # sequence 0's host query length is wrong
+    got = _run(q, kc, vc, md, 0.125)
+    assert torch.isnan(got[:200]).any()
+    _assert_close(got[200:], ref[200:], torch.float16)
+
+
 def test_prefill_invalid_block_id_poisons_only_its_sequence():
     seqs = [300, 64]
     kc, vc, tables, _ = build_paged(seqs, 32, 16, 2, 64, dtype=torch.float16)
@@ -380,6 +404,23 @@ def test_graph_replays_match_eager(config):
             again = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
             torch.cuda.synchronize()
             assert torch.equal(again, eager)
+
+
+def test_workspace_reused_across_shapes():
+    """One workspace (per stream) serves calls of different shapes back to
+    back: partials of one call never land on another call's counters."""
+    cases = [
+        ([37 + (13 * i) % 900 for i in range(60)], None),   # decode, many split pairs
+        ([4000, 900, 35], [300, 900, 1]),                   # prefill splits + decode rows
+        ([5, 17], None),                                    # tiny decode
+        ([2500, 64], [64, 64]),                             # prefill splits again
+    ]
+    for _ in range(2):
+        for seqs, qls in cases:
+            qls = qls or [1] * len(seqs)
+            q, kc, vc, md, _, _ = _case(seqs, qls, 14, 2, 64, 16, torch.float16)
+            _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125),
+                          torch.float16, f"{len(seqs)} seqs")
 
 
 def test_rejects_unsupported_shapes():

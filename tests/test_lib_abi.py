@@ -45,7 +45,7 @@ def test_status_strings_and_version():
 
 def _attn_args(**over):
     a = dict(out=16, query=16, k_cache=16, v_cache=16, bt=16, bt_stride=4, bt_width=4, bt64=0,
-             sl=16, sl64=0, qsl=16, qsl64=0, slh=None, slh64=0, S=2, T=2, maxq=1, maxs=64, decode_only=1,
+             sl=16, sl64=0, qsl=16, qsl64=0, slh=None, slh64=0, qslh=None, qslh64=0, S=2, T=2, maxq=1, maxs=64, decode_only=1,
              Hq=14, Hkv=2, D=64, bs=16, nb=32, scale=0.125, dtype=_lib.NS_DTYPE_F16,
              ws=16, ws_bytes=1 << 30, stream=None)
     a.update(over)
