@@ -49,7 +49,8 @@ struct AttnParams {
   int64_t num_blocks;
   int64_t max_ctx;        // tokens addressable through a table row
   float scale_log2;       // scale * log2(e): softmax runs in base 2
-  int split_tokens;       // decode: context tokens per workgroup
+  int split_tokens;       // decode: context tokens per workgroup (pair plans: the base, shifted per pair)
+  int split_tokens_max;   // decode, host side: the longest split any workgroup takes
   int max_splits;         // decode: workgroups per (sequence, kv head)
   int skip_decode_rows;   // varlen: one-row sequences belong to the decode kernel
   float* part_o;          // [S, Hkv, max_splits, G, D]  unnormalised partial outputs
@@ -61,9 +62,13 @@ struct AttnParams {
   float* pf_part;
   int pf_part_bytes;
   unsigned* pf_counters;
-  int plan_n;             // decode: workgroups listed in plan; prefill: sequences listed (0: no plan)
-  // Decode schedule from host-side lengths: entry x = s | kvh << 16 | split << 20 |
-  // (nsplit - 1) << 26 for workgroup x, or kPlanEmpty.
+  int plan_n;             // decode: workgroups in the planned grid; prefill: sequences listed (0: no plan)
+  int plan_pairs;         // decode: 0 = one plan entry per workgroup, else pairs listed
+  // Decode schedule from host-side lengths, either one entry per workgroup x,
+  // s | kvh << 16 | split << 20 | (nsplit - 1) << 26 or kPlanEmpty, or (long
+  // contexts) one entry pair per (sequence, kv head): plan[0..8] are the
+  // per-XCD offsets into the pair list, pair k is plan[9 + 2k] = s | kvh << 16 |
+  // (nsplit - 1) << 20 and plan[10 + 2k] = its first workgroup index on its XCD.
   // Prefill schedule (its own copy of the parameters): two entries per listed
   // sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
   // slot_base | pair_base << 16.
@@ -209,13 +214,32 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   __shared__ int s_last;
 
   int s, split, kvh, nsplit_plan = 0;
-  if (p.plan_n > 0) {
+  int split_tok = p.split_tokens;
+  if (p.plan_n > 0 && p.plan_pairs == 0) {
     const uint32_t e = p.plan[blockIdx.x];
     if (e == kPlanEmpty) return;
     s = static_cast<int>(e & 0xFFFFu);
     kvh = static_cast<int>((e >> 16) & 0xFu);
     split = static_cast<int>((e >> 20) & 0x3Fu);
     nsplit_plan = static_cast<int>(e >> 26) + 1;
+  } else if (p.plan_n > 0) {
+    // Pair list: workgroup x is the (x / 8)-th of XCD x % 8; find the pair
+    // whose splits cover it (binary search over first-workgroup indices).
+    const int x = static_cast<int>(blockIdx.x & 7u), idx = static_cast<int>(blockIdx.x >> 3);
+    int lo = static_cast<int>(p.plan[x]), hi = static_cast<int>(p.plan[x + 1]);
+    if (lo >= hi) return;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (static_cast<int>(p.plan[10 + 2 * mid] & 0x3FFFFFFu) <= idx) lo = mid;
+      else hi = mid;
+    }
+    const uint32_t e = p.plan[9 + 2 * lo], f = p.plan[10 + 2 * lo];
+    nsplit_plan = static_cast<int>(e >> 20) + 1;
+    split = idx - static_cast<int>(f & 0x3FFFFFFu);
+    split_tok = p.split_tokens << (f >> 26);
+    if (split >= nsplit_plan) return;  // past the last pair of this XCD
+    s = static_cast<int>(e & 0xFFFFu);
+    kvh = static_cast<int>((e >> 16) & 0xFu);
   } else {
     split = blockIdx.x;
     kvh = blockIdx.y;
@@ -225,8 +249,8 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   const int G = p.group, Hkv = p.num_kv_heads;
   const int bs_mask = (1 << p.bs_shift) - 1;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
-  const int64_t t_split0 = static_cast<int64_t>(split) * p.split_tokens;
-  const int64_t t_cap = p.max_ctx < t_split0 + p.split_tokens ? p.max_ctx : t_split0 + p.split_tokens;
+  const int64_t t_split0 = static_cast<int64_t>(split) * split_tok;
+  const int64_t t_cap = p.max_ctx < t_split0 + split_tok ? p.max_ctx : t_split0 + split_tok;
 
   // Loads that do not depend on the context length go out together: the
   // length, this wave's first block-table entries and (decode-only) Q.
@@ -264,7 +288,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 
   const int64_t L = L_raw < p.max_ctx ? L_raw : p.max_ctx;
   T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
-  const int nsplit_len = static_cast<int>((L + p.split_tokens - 1) / p.split_tokens);
+  const int nsplit_len = static_cast<int>((L + split_tok - 1) / split_tok);
   // The splits that arrive at this pair's merge.  A plan fixes them from the
   // host lengths, so every launched workgroup arrives even if the device
   // length is shorter; a device length the plan does not cover is a broken
@@ -279,7 +303,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
       for (int i = tid; i < G * D; i += THREADS) out_row[i] = static_cast<T>(0.f);
     return;
   }
-  const int64_t t_split1 = L < t_split0 + p.split_tokens ? L : t_split0 + p.split_tokens;
+  const int64_t t_split1 = L < t_split0 + split_tok ? L : t_split0 + split_tok;
 
   T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
   float m_run = -INFINITY, l_run = 0.f;
@@ -1162,7 +1186,7 @@ hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool l
   // Workgroups whose waves take several steps pipeline their K/V loads
   // (double-buffered registers, fewer resident waves); one-step workgroups
   // keep the lean variant and its occupancy.
-  const bool pipe = p.split_tokens > W * CH;
+  const bool pipe = p.split_tokens_max > W * CH;
   const void* dk =
       p.bt64 ? (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, true>)
                      : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, false>))
@@ -1245,12 +1269,76 @@ int build_decode_plan_for(AttnParams& p, const std::vector<std::pair<int64_t, in
     for (int x = 0; x < kXcds; ++x)
       p.plan[k * kXcds + x] = k < bucket[x].size() ? bucket[x][k] : kPlanEmpty;
   p.split_tokens = split;
+  p.split_tokens_max = split;
+  return static_cast<int>(rows * kXcds);
+}
+
+// Pair-list plan at a given split: the same XCD bin-packing as above, but
+// one kernel-argument entry pair per (sequence, kv head) instead of one entry
+// per workgroup, so long contexts keep short splits (the dispatcher then
+// balances the tail) without overflowing the kernel arguments.
+// A pair's split is the base, doubled until the pair has at most
+// kMaxPairSplits splits: the last split to arrive merges them all, and that
+// merge's length grows with their number.
+constexpr int kPairMax = (kPlanMax - 9) / 2;
+constexpr int kMaxPairSplits = 64;
+
+int build_decode_pair_plan(AttnParams& p, const std::vector<std::pair<int64_t, int>>& order, int split) {
+  constexpr int kXcds = 8;
+  if (static_cast<int64_t>(order.size()) * p.num_kv_heads > kPairMax) return 0;
+  struct Item {
+    uint32_t e;
+    int64_t n;
+    int shift;
+  };
+  std::vector<Item> bucket[kXcds];
+  int64_t load[kXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int max_shift = 0;
+  for (const auto& [L, i] : order) {
+    int shift = 0;
+    while ((L + (static_cast<int64_t>(split) << shift) - 1) / (static_cast<int64_t>(split) << shift) > kMaxPairSplits)
+      ++shift;
+    if (shift > 20) return 0;
+    const int64_t sp = static_cast<int64_t>(split) << shift;
+    int64_t n = (L + sp - 1) / sp;
+    n = n < 1 ? 1 : n;
+    max_shift = shift > max_shift ? shift : max_shift;
+    for (int kvh = 0; kvh < p.num_kv_heads; ++kvh) {
+      int b = 0;
+      for (int x = 1; x < kXcds; ++x)
+        if (load[x] < load[b]) b = x;
+      load[b] += L + sp / 4;
+      bucket[b].push_back({static_cast<uint32_t>(i) | static_cast<uint32_t>(kvh) << 16 |
+                               static_cast<uint32_t>(n - 1) << 20,
+                           n, shift});
+    }
+  }
+  int k = 0;
+  int64_t rows = 0;
+  for (int x = 0; x < kXcds; ++x) {
+    p.plan[x] = static_cast<uint32_t>(k);
+    int64_t first = 0;
+    for (const Item& it : bucket[x]) {
+      if (first > 0x3FFFFFF) return 0;
+      p.plan[9 + 2 * k] = it.e;
+      p.plan[10 + 2 * k] = static_cast<uint32_t>(first) | static_cast<uint32_t>(it.shift) << 26;
+      first += it.n;
+      ++k;
+    }
+    rows = first > rows ? first : rows;
+  }
+  p.plan[kXcds] = static_cast<uint32_t>(k);
+  if (rows * kXcds > 0x7FFFFFFF) return 0;
+  p.split_tokens = split;
+  p.split_tokens_max = split << max_shift;
+  p.plan_pairs = k;
   return static_cast<int>(rows * kXcds);
 }
 
 // The split starts at the workspace layout's (so at most max_splits per
-// sequence) and doubles until the batch fits the plan: long contexts get
-// long splits, whose waves then pipeline their steps.
+// sequence).  If one entry per workgroup does not fit, a pair-list plan keeps
+// that split; failing that, the split doubles until the batch fits: long
+// contexts then get long splits, whose waves pipeline their steps.
 int64_t host_index(const void* a, int is64, int64_t i) {
   return is64 ? static_cast<const int64_t*>(a)[i] : static_cast<const int32_t*>(a)[i];
 }
@@ -1270,6 +1358,13 @@ int build_decode_plan(AttnParams& p, const void* lens, int lens64, const void* q
   if (order.empty()) return -1;
   std::stable_sort(order.begin(), order.end(),
                    [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a.first > b.first; });
+  p.plan_pairs = 0;
+  {
+    const int n = build_decode_plan_for(p, order, p.split_tokens);
+    if (n > 0) return n;
+    const int np = build_decode_pair_plan(p, order, p.split_tokens);
+    if (np > 0) return np;
+  }
   for (int64_t split = p.split_tokens;; split *= 2) {
     const int n = build_decode_plan_for(p, order, static_cast<int>(split));
     if (n > 0) return n;
@@ -1458,6 +1553,7 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   p.max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.split_tokens = plan.split_tokens;
+  p.split_tokens_max = plan.split_tokens;
   p.max_splits = plan.max_splits;
   p.skip_decode_rows = 1;
   char* ws = static_cast<char*>(workspace);
@@ -1470,6 +1566,7 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   p.pf_part = reinterpret_cast<float*>(ws + wl.pf_part_off);
   p.pf_part_bytes = static_cast<int>(wl.pf_part_bytes);
   p.plan_n = 0;
+  p.plan_pairs = 0;
   // Decode plan from the host lengths.  Without host query offsets a mixed
   // batch's plan covers every sequence and the workgroups of sequences with
   // more than one query row leave at once (the prefill kernel owns them).
