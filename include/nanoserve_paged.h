@@ -76,6 +76,40 @@ int ns_reshape_and_cache(const void* key, const void* value,
                          int src_dtype, int cache_dtype, void* stream);
 
 /*
+ * ns_rope_reshape_and_cache -- rotary embedding of Q and K fused with the
+ * paged-cache write of K and V (the two steps before attention at the
+ * reference call site, nanoserve/qwen2.py:53-57).
+ *
+ * Replaces RotaryEmbedding.apply (reference nanoserve/layers.py:84-88):
+ *     q' = q * cos + rotate_half(q) * sin,  k' likewise,
+ *     rotate_half(x) = cat(-x[..., D/2:], x[..., :D/2]),
+ * followed by PagedKVCache.write (reference nanoserve/kv_cache.py:73-81) of
+ * k' and v through slot_mapping, in one launch.  q' is written to q_out
+ * ([num_tokens, num_heads, head_dim] contiguous; q_out may equal query when
+ * query is contiguous); k' is only written to the cache, as in the
+ * reference, where the rotated k has no other use.
+ *
+ * cos and sin are the per-forward lookups of the reference
+ * (RotaryEmbedding.cos_sin, layers.py:75-79): [num_tokens, head_dim] rows in
+ * the model dtype `dtype` with token stride cos_sin_stride_token.  The result
+ * is bit-exact with the reference's tensor arithmetic (each product and the
+ * sum rounded to `dtype`, then `.to(cache_dtype)`).  Slots outside
+ * [0, num_blocks*block_size) are skipped.  All pointers must be 16-byte
+ * aligned and all strides (in elements) multiples of 16 bytes' worth of
+ * elements; head_dim must be a multiple of 2 * (16 / dtype size).
+ */
+int ns_rope_reshape_and_cache(void* q_out, const void* query,
+                              int64_t q_stride_token, int64_t q_stride_head,
+                              const void* key, int64_t key_stride_token, int64_t key_stride_head,
+                              const void* value, int64_t value_stride_token, int64_t value_stride_head,
+                              const void* cos, const void* sin, int64_t cos_sin_stride_token,
+                              void* k_cache, void* v_cache,
+                              const void* slot_mapping, int slot_mapping_is_int64,
+                              int64_t num_tokens, int num_heads, int num_kv_heads, int head_dim,
+                              int block_size, int64_t num_blocks,
+                              int dtype, int cache_dtype, void* stream);
+
+/*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
  * ns_paged_attention needs for these sizes (split-K partials and counters).
  * Without is_decode_only it includes the prefill split state: a fixed 512

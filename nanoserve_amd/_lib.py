@@ -47,6 +47,17 @@ SIGNATURES = {
         c_int64, c_int, c_int, c_int, c_int64,   # T, Hkv, D, block_size, num_blocks
         c_int, c_int, c_void_p,                  # src dtype, cache dtype, stream
     ]),
+    "ns_rope_reshape_and_cache": (c_int, [
+        c_void_p, c_void_p, c_int64, c_int64,    # q_out, query, query token / head strides
+        c_void_p, c_int64, c_int64,              # key, token / head strides
+        c_void_p, c_int64, c_int64,              # value, token / head strides
+        c_void_p, c_void_p, c_int64,             # cos, sin, token stride
+        c_void_p, c_void_p,                      # k_cache, v_cache
+        c_void_p, c_int,                         # slot_mapping, is_int64
+        c_int64, c_int, c_int, c_int,            # T, Hq, Hkv, D
+        c_int, c_int64,                          # block_size, num_blocks
+        c_int, c_int, c_void_p,                  # model dtype, cache dtype, stream
+    ]),
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,
     ]),

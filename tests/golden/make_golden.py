@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 sys.path.insert(0, ROOT)
 
 from oracle.paged_attention import dense_reference, paged_attention_ref, reshape_and_cache_ref  # noqa: E402
+from oracle.rope import rope_cos_sin_ref, rope_reshape_and_cache_ref, rope_table_ref  # noqa: E402
 from tests._helpers import build_paged, make_md  # noqa: E402
 
 # name: (seq_lens, query_lens, Hq, Hkv, D, block_size, dtype)
@@ -81,10 +82,40 @@ def cache_write_fixture():
                 slot_mapping=slots.numpy(), expected_k=_np(ek), expected_v=_np(ev))
 
 
+# name: (T, Hq, Hkv, D, num_blocks, block_size, base, dtype)
+ROPE_CASES = {
+    "fp16_d64": (13, 14, 2, 64, 4, 16, 10000.0, torch.float16),
+    "bf16_d128": (9, 28, 4, 128, 3, 32, 1000000.0, torch.bfloat16),
+}
+
+
+def rope_fixture(name):
+    """Fused rotary + cache write: inputs, positions, slots (one -1) and the oracle's outputs."""
+    T, hq, hkv, d, nb, bs, base, dt = ROPE_CASES[name]
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(T, hq, d, generator=g).to(dt)
+    k = torch.randn(T, hkv, d, generator=g).to(dt)
+    v = torch.randn(T, hkv, d, generator=g).to(dt)
+    pos = torch.randint(0, 4096, (T,), generator=g)
+    cos_t, sin_t = rope_table_ref(d, 4096, base)
+    cos, sin = rope_cos_sin_ref(cos_t, sin_t, pos, dt)
+    kc = torch.randn(nb, bs, hkv, d, generator=g).to(dt)
+    vc = torch.randn(nb, bs, hkv, d, generator=g).to(dt)
+    slots = torch.randperm(nb * bs, generator=g)[:T].to(torch.int64)
+    slots[T // 2] = -1
+    qr, ek, ev = rope_reshape_and_cache_ref(q, k, v, cos, sin, kc, vc, slots)
+    return dict(dtype=np.array(str(dt).replace("torch.", "")), base=np.array(base, np.float64),
+                positions=pos.numpy(), query=_np(q), key=_np(k), value=_np(v), cos=_np(cos), sin=_np(sin),
+                k_cache=_np(kc), v_cache=_np(vc), slot_mapping=slots.numpy(),
+                expected_q=_np(qr), expected_k=_np(ek), expected_v=_np(ev))
+
+
 def main():
     for name in ATTN_CASES:
         np.savez_compressed(os.path.join(HERE, f"attn_{name}.npz"), **attn_fixture(name))
     np.savez_compressed(os.path.join(HERE, "cache_write_f32_to_f16.npz"), **cache_write_fixture())
+    for name in ROPE_CASES:
+        np.savez_compressed(os.path.join(HERE, f"rope_{name}.npz"), **rope_fixture(name))
     print("wrote", sorted(f for f in os.listdir(HERE) if f.endswith(".npz")))
 
 

@@ -18,9 +18,11 @@ import torch
 
 from nanoserve_amd.attention import AttentionMetadata
 from oracle.paged_attention import paged_attention_ref, reshape_and_cache_ref
+from oracle.rope import rope_cos_sin_ref, rope_reshape_and_cache_ref, rope_table_ref
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 ATTN = sorted(glob.glob(os.path.join(HERE, "attn_*.npz")))
+ROPE = sorted(glob.glob(os.path.join(HERE, "rope_*.npz")))
 TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2}
 
 
@@ -50,6 +52,7 @@ def load_attn(path, device="cpu"):
 def test_fixtures_present():
     assert len(ATTN) >= 4
     assert os.path.exists(os.path.join(HERE, "cache_write_f32_to_f16.npz"))
+    assert len(ROPE) >= 2
 
 
 @pytest.mark.parametrize("path", ATTN, ids=[os.path.basename(p)[5:-4] for p in ATTN])
@@ -91,3 +94,41 @@ def test_hip_cache_write_matches_golden():
                       torch.from_numpy(z["slot_mapping"]).cuda())
     np.testing.assert_array_equal(kc.cpu().view(torch.int16).numpy().view(np.uint16), z["expected_k"])
     np.testing.assert_array_equal(vc.cpu().view(torch.int16).numpy().view(np.uint16), z["expected_v"])
+
+
+def load_rope(path, device="cpu"):
+    z = np.load(path, allow_pickle=False)
+    dt = {"float16": torch.float16, "bfloat16": torch.bfloat16}[str(z["dtype"])]
+    t = {n: _half(z[n], dt).to(device) for n in ("query", "key", "value", "cos", "sin", "k_cache", "v_cache")}
+    return z, dt, t, torch.from_numpy(z["slot_mapping"]).to(device)
+
+
+def _bits16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize("path", ROPE, ids=[os.path.basename(p)[5:-4] for p in ROPE])
+def test_oracle_reproduces_golden_rope(path):
+    z, dt, t, slots = load_rope(path)
+    d = t["query"].shape[-1]
+    cos_t, sin_t = rope_table_ref(d, 4096, float(z["base"]))
+    cos, sin = rope_cos_sin_ref(cos_t, sin_t, torch.from_numpy(z["positions"]), dt)
+    np.testing.assert_array_equal(_bits16(cos), z["cos"])
+    np.testing.assert_array_equal(_bits16(sin), z["sin"])
+    qr, ek, ev = rope_reshape_and_cache_ref(t["query"], t["key"], t["value"], cos, sin,
+                                            t["k_cache"], t["v_cache"], slots)
+    for got, name in ((qr, "expected_q"), (ek, "expected_k"), (ev, "expected_v")):
+        np.testing.assert_array_equal(_bits16(got), z[name])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("path", ROPE, ids=[os.path.basename(p)[5:-4] for p in ROPE])
+def test_hip_rope_matches_golden(path):
+    from nanoserve_amd import rope_reshape_and_cache
+
+    z, dt, t, slots = load_rope(path, "cuda")
+    qr = rope_reshape_and_cache(t["query"], t["key"], t["value"], t["cos"], t["sin"],
+                                t["k_cache"], t["v_cache"], slots)
+    torch.cuda.synchronize()
+    for got, name in ((qr, "expected_q"), (t["k_cache"], "expected_k"), (t["v_cache"], "expected_v")):
+        np.testing.assert_array_equal(_bits16(got), z[name])

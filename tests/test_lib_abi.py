@@ -24,6 +24,7 @@ def _declared_functions() -> list[str]:
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for n in ("ns_reshape_and_cache", "ns_paged_attention", "ns_paged_attention_workspace_size",
+              "ns_rope_reshape_and_cache",
               "ns_error_string", "ns_version"):
         assert n in names
 
@@ -110,3 +111,37 @@ def test_reshape_and_cache_rejects_bad_arguments(over, code):
 def test_reshape_and_cache_zero_tokens_is_a_no_op():
     lib = _lib.load()
     assert lib.ns_reshape_and_cache(*_rc_args(T=0, key=None)) == _lib.NS_OK
+
+
+def _rope_args(**over):
+    a = dict(qo=16, q=16, qst=14 * 64, qsh=64, k=16, kst=128, ksh=64, v=16, vst=128, vsh=64,
+             cos=16, sin=16, cst=64, kc=16, vc=16, slots=16, s64=1,
+             T=4, Hq=14, Hkv=2, D=64, bs=16, nb=8, dt=_lib.NS_DTYPE_F16, cdt=_lib.NS_DTYPE_F16, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(q=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(cos=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(slots=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(Hq=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(nb=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(dt=7), _lib.NS_ERR_UNSUPPORTED),
+    (dict(cdt=7), _lib.NS_ERR_UNSUPPORTED),
+    (dict(D=72), _lib.NS_ERR_UNSUPPORTED),               # half a row not a whole number of 16-byte chunks
+    (dict(D=68, dt=_lib.NS_DTYPE_F32, qst=14 * 68, qsh=68, kst=136, ksh=68, vst=136, vsh=68, cst=68),
+     _lib.NS_ERR_UNSUPPORTED),                           # f32: 4 per chunk, 34 per half
+    (dict(qsh=60), _lib.NS_ERR_INVALID_ARG),             # stride not a whole number of chunks
+    (dict(cst=4), _lib.NS_ERR_INVALID_ARG),
+    (dict(k=18), _lib.NS_ERR_INVALID_ARG),               # misaligned row base
+    (dict(sin=24), _lib.NS_ERR_INVALID_ARG),
+])
+def test_rope_reshape_and_cache_rejects_bad_arguments(over, code):
+    lib = _lib.load()
+    assert lib.ns_rope_reshape_and_cache(*_rope_args(**over)) == code
+
+
+def test_rope_reshape_and_cache_zero_tokens_is_a_no_op():
+    lib = _lib.load()
+    assert lib.ns_rope_reshape_and_cache(*_rope_args(T=0, q=None, k=None)) == _lib.NS_OK
