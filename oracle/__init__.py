@@ -7,6 +7,9 @@ path so the HIP kernels can be checked against it:
   dense_reference       reference tests/test_paged_attention.py:24-36 (fp64 textbook)
   reshape_and_cache_ref reference nanoserve/kv_cache.py:73-81 (.to() + index_copy_)
   slot_mapping_ref      reference nanoserve/block_manager.py:131-132 (closed form)
+  rope.*                reference nanoserve/layers.py:65-90 (rotary table and
+                        apply) and qwen2.py:53-57 (rotary, then cache write);
+                        pinned in tests/test_oracle_rope.py
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import it, and only as the checker (or the timed CPU baseline), never as the
