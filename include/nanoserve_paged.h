@@ -110,6 +110,28 @@ int ns_rope_reshape_and_cache(void* q_out, const void* query,
                               int dtype, int cache_dtype, void* stream);
 
 /*
+ * ns_int4_linear -- out = x · W^T + bias with W held as group-wise asymmetric
+ * INT4, dequantised in registers inside the GEMM.
+ *
+ * Replaces QuantLinear.forward in "int4" mode (reference
+ * nanoserve/quant.py:157-158: F.linear(x, dequantize_int4(...), bias),
+ * dequantize_int4 at quant.py:83-95), with the weight format of
+ * quantize_int4_groupwise (quant.py:53-80):
+ *   qweight [N, K/2] uint8, code of (n, k) in the low nibble of byte k/2 for
+ *           even k and in the high nibble for odd k;
+ *   scales  [N, K/group_size] float32;  zeros [N, K/group_size] uint8;
+ *   w(n, k) = (code - zero) * scale in float32, rounded to `dtype`.
+ * x is [M, K] with row stride x_stride_row (elements, a multiple of 8, rows
+ * 16-byte aligned); out is [M, N] contiguous (8-byte aligned); bias is [N]
+ * in `dtype` or NULL.  Accumulation is fp32 (MFMA); out = round(acc + bias).
+ * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16.  N must be a multiple of 16, K and
+ * group_size multiples of 32 with K a multiple of group_size.
+ */
+int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
+                   const void* qweight, const void* scales, const void* zeros, const void* bias,
+                   int64_t M, int N, int K, int group_size, int dtype, void* stream);
+
+/*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
  * ns_paged_attention needs for these sizes (split-K partials and counters).
  * Without is_decode_only it includes the prefill split state: a fixed 512

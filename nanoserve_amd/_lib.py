@@ -58,6 +58,12 @@ SIGNATURES = {
         c_int, c_int64,                          # block_size, num_blocks
         c_int, c_int, c_void_p,                  # model dtype, cache dtype, stream
     ]),
+    "ns_int4_linear": (c_int, [
+        c_void_p, c_void_p, c_int64,             # out, x, x row stride
+        c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)
+        c_int64, c_int, c_int, c_int,            # M, N, K, group_size
+        c_int, c_void_p,                         # dtype, stream
+    ]),
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,
     ]),

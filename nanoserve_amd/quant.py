@@ -1,0 +1,172 @@
+"""INT4 group-wise weight quantisation with a fused dequant-GEMM.
+
+Keeps the reference's "int4" format (nanoserve/quant.py:53-80): per output
+row, groups of `group_size` consecutive input features share a float32 scale
+and a uint8 zero point, codes are round(w / scale) + zero clamped to [0, 15],
+and two codes share a byte (even input index in the low nibble).  The
+quantiser is setup-time tensor code and follows the reference step for step,
+so checkpoints quantised either way are interchangeable.
+
+The difference is the forward.  The reference's QuantLinear expands the whole
+weight to fp16 on every call and then runs F.linear (quant.py:149-158); here
+`Int4Linear.forward` calls `ns_int4_linear`, which dequantises each weight in
+registers on its way into the MFMA and never writes the expanded weight.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+
+@torch.no_grad()
+def quantize_int4_groupwise(w: torch.Tensor, group_size: int = 128):
+    """w [out, in] -> (packed uint8 [out, in/2], scales f32 [out, G], zeros uint8 [out, G]).
+
+    Same steps as the reference (quant.py:53-80): scale = (max - min) / 15
+    clamped to 1e-8, zero = round(-min / scale) clamped to [0, 15],
+    code = clamp(round(w / scale) + zero, 0, 15), round half to even.
+    """
+    out_f, in_f = w.shape
+    if in_f % group_size != 0:
+        raise ValueError(f"in_features {in_f} not divisible by group_size {group_size}")
+    if in_f % 2 != 0:
+        raise ValueError("in_features must be even to pack two nibbles per byte")
+    g = in_f // group_size
+    wg = w.to(torch.float32).reshape(out_f, g, group_size)
+    w_max = wg.amax(dim=2, keepdim=True)
+    w_min = wg.amin(dim=2, keepdim=True)
+    scale = ((w_max - w_min) / 15.0).clamp(min=1e-8)
+    zero = (-w_min / scale).round().clamp(0, 15)
+    q = ((wg / scale).round() + zero).clamp(0, 15).to(torch.uint8).reshape(out_f, in_f)
+    packed = (q[:, 0::2] | (q[:, 1::2] << 4)).contiguous()
+    return packed, scale.squeeze(2).contiguous(), zero.squeeze(2).to(torch.uint8).contiguous()
+
+
+@torch.inference_mode()
+def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+                bias: torch.Tensor | None, group_size: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [..., K] -> [..., N] through ns_int4_linear (HIP; no CPU fallback)."""
+    lib = _lib.load()
+    N, half_k = qweight.shape
+    K = 2 * half_k
+    if x.shape[-1] != K:
+        raise ValueError(f"x has {x.shape[-1]} features, the weight {K}")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"int4_linear computes in fp16 or bf16, got {x.dtype}")
+    if not (x.is_cuda and qweight.is_cuda and scales.is_cuda and zeros.is_cuda):
+        raise ValueError("int4_linear needs GPU tensors (the HIP path has no CPU fallback)")
+    if qweight.dtype != torch.uint8 or zeros.dtype != torch.uint8 or scales.dtype != torch.float32:
+        raise TypeError("qweight/zeros must be uint8 and scales float32")
+    if not (qweight.is_contiguous() and scales.is_contiguous() and zeros.is_contiguous()):
+        raise ValueError("quantised weight tensors must be contiguous")
+    if bias is not None and (bias.dtype != x.dtype or bias.shape != (N,) or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous [{N}] {x.dtype} tensor")
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    if x2.stride(1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
+        x2 = x2.contiguous()
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    elif out.shape != (M, N) or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{M}, {N}] {x.dtype} tensor")
+    rc = lib.ns_int4_linear(out.data_ptr(), x2.data_ptr(), x2.stride(0),
+                            qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
+                            bias.data_ptr() if bias is not None else None,
+                            M, N, K, group_size, _lib.DTYPE_CODES[x.dtype],
+                            torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(rc, "ns_int4_linear")
+    return out.view(*lead, N)
+
+
+class Int4Linear(nn.Module):
+    """Drop-in nn.Linear whose weight lives as INT4 groups (reference QuantLinear, int4 mode).
+
+    Buffers and their shapes match the reference module (quant.py:131-135):
+    qweight [out, in/2] uint8, scales [out, in/gs] float32, zeros [out, in/gs]
+    uint8, plus an optional bias in the compute dtype.
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool, group_size: int, dtype, device) -> None:
+        super().__init__()
+        if in_features % group_size != 0:
+            raise ValueError(f"in_features {in_features} not divisible by group_size {group_size}")
+        self.in_features = in_features
+        self.out_features = out_features
+        self.group_size = group_size
+        self.compute_dtype = dtype
+        g = in_features // group_size
+        self.register_buffer("qweight", torch.zeros(out_features, in_features // 2, dtype=torch.uint8, device=device))
+        self.register_buffer("scales", torch.zeros(out_features, g, dtype=torch.float32, device=device))
+        self.register_buffer("zeros", torch.zeros(out_features, g, dtype=torch.uint8, device=device))
+        self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype, device=device)) if bias else None
+
+    @classmethod
+    def from_linear(cls, lin: nn.Linear, group_size: int = 128) -> "Int4Linear":
+        w = lin.weight.data
+        m = cls(lin.in_features, lin.out_features, lin.bias is not None, group_size, w.dtype, w.device)
+        packed, s, z = quantize_int4_groupwise(w, group_size)
+        m.qweight.copy_(packed)
+        m.scales.copy_(s)
+        m.zeros.copy_(z)
+        if lin.bias is not None:
+            m.bias.data.copy_(lin.bias.data)
+        return m
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return int4_linear(x, self.qweight, self.scales, self.zeros,
+                           None if self.bias is None else self.bias.data, self.group_size)
+
+    def extra_repr(self) -> str:
+        return f"in={self.in_features}, out={self.out_features}, int4 group={self.group_size}"
+
+
+def quantize_model(model: nn.Module, group_size: int = 128, skip: tuple[str, ...] = ("lm_head",)) -> dict:
+    """Replace every eligible nn.Linear with Int4Linear in place (reference quant.py:165-199, int4).
+
+    Linears whose in_features is not a multiple of group_size, or whose
+    out_features is not a multiple of 16 (the kernel's row tile), are left as
+    they are.  Returns a memory report like the reference's.
+    """
+    before = _weight_bytes(model)
+    replaced = 0
+
+    def visit(module: nn.Module, prefix: str = "") -> None:
+        nonlocal replaced
+        for name, child in list(module.named_children()):
+            full = f"{prefix}.{name}" if prefix else name
+            if any(s in full for s in skip):
+                continue
+            if isinstance(child, nn.Linear):
+                if child.in_features % group_size != 0 or child.out_features % 16 != 0:
+                    continue
+                setattr(module, name, Int4Linear.from_linear(child, group_size))
+                replaced += 1
+            else:
+                visit(child, full)
+
+    visit(model)
+    after = _weight_bytes(model)
+    return {
+        "mode": "int4",
+        "group_size": group_size,
+        "layers_quantized": replaced,
+        "weight_mib_before": before / 2**20,
+        "weight_mib_after": after / 2**20,
+        "compression": before / after if after else 0.0,
+        "freed_mib": (before - after) / 2**20,
+    }
+
+
+def _weight_bytes(model: nn.Module) -> int:
+    seen = set()
+    total = 0
+    for t in list(model.parameters()) + list(model.buffers()):
+        if id(t) in seen:
+            continue
+        seen.add(id(t))
+        total += t.numel() * t.element_size()
+    return total

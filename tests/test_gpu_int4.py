@@ -1,0 +1,130 @@
+"""HIP INT4 dequant-GEMM (ns_int4_linear) against the oracle (MI355X).
+
+The weights the MFMA sees must be the reference's dequantised weights bit for
+bit (checked through an identity input, whose products are exact), and the
+output must equal x · W^T + bias rounded once to the model dtype: within one
+rounding of the float64 result (|err| <= 2^-10 |ref| for fp16, 2^-7 |ref| for
+bf16, plus an absolute 1e-5 · max|ref| for fp32 accumulation order).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nanoserve_amd.quant import Int4Linear, int4_linear, quantize_int4_groupwise, quantize_model
+from oracle.quant import dequantize_int4_ref, int4_linear_ref
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
+NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
+
+# Qwen2.5-0.5B projections (in -> out): q, k/v, o, gate/up, down, and fused q|k|v, gate|up.
+QWEN = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 1152), (896, 9728)]
+
+
+def _weights(N, K, gs, seed, scale=0.05):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * scale
+    return quantize_int4_groupwise(w, gs)
+
+
+def _check(got: torch.Tensor, ref: np.ndarray, dtype, what=""):
+    got = got.float().cpu().numpy().astype(np.float64)
+    tol = RTOL[dtype] * np.abs(ref) + 1e-5 * max(1.0, np.abs(ref).max())
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (f"{what}: {bad.sum()} of {bad.size} outside one rounding; "
+                           f"max err {np.abs(got - ref).max():.3e}")
+
+
+def _run(M, N, K, dtype, gs=128, bias=True, seed=0, x_scale=1.0):
+    packed, s, z = _weights(N, K, gs, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = (torch.randn(M, K, generator=g) * x_scale).to(dtype)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype) if bias else None
+    got = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), None if b is None else b.to(DEV), gs)
+    torch.cuda.synchronize()
+    w = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), gs, NAME[dtype])
+    ref = int4_linear_ref(x.float().numpy(), w, None if b is None else b.float().numpy())
+    _check(got, ref, dtype, f"M={M} N={N} K={K} {dtype}")
+    return got, x, (packed, s, z), b
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K,N", QWEN, ids=[f"{k}x{n}" for k, n in QWEN])
+@pytest.mark.parametrize("M", [1, 32])
+def test_decode_shapes(dtype, K, N, M):
+    print(f"int4 M={M} N={N} K={K} {dtype}", flush=True)
+    _run(M, N, K, dtype, seed=M + N)
+
+
+@pytest.mark.parametrize("M", [7, 17, 33, 64, 100, 2076])
+def test_row_counts_across_tiles(M):
+    _run(M, 1152, 896, torch.float16, seed=M)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+def test_group_sizes(gs):
+    _run(20, 256, 512, torch.float16, gs=gs, seed=gs)
+
+
+def test_without_bias():
+    _run(9, 128, 896, torch.bfloat16, bias=False)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_identity_input_reproduces_dequantised_weights_bit_exactly(dtype):
+    """x = I: y[m][n] = W[n][m] (one exact product per output), so y^T is the dequantised weight."""
+    K, N, gs = 128, 64, 128
+    packed, s, z = _weights(N, K, gs, 3, scale=1.0)
+    eye = torch.eye(K, dtype=dtype, device=DEV)
+    y = int4_linear(eye, packed.to(DEV), s.to(DEV), z.to(DEV), None, gs)
+    torch.cuda.synchronize()
+    want = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), gs, NAME[dtype])
+    assert np.array_equal(y.float().cpu().numpy().T, want)
+
+
+def test_strided_rows_and_leading_dims():
+    """x as a column slice of a wider activation, with a [B, T, K] leading shape."""
+    K, N = 896, 1152
+    packed, s, z = _weights(N, K, 128, 5)
+    g = torch.Generator().manual_seed(6)
+    wide = torch.randn(2, 11, K + 64, generator=g).half()
+    x = wide[..., 64:]
+    got = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), None, 128)
+    torch.cuda.synchronize()
+    assert got.shape == (2, 11, N)
+    w = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), 128, "float16")
+    ref = int4_linear_ref(x.reshape(-1, K).float().numpy(), w, None)
+    _check(got.reshape(-1, N), ref, torch.float16, "strided")
+
+
+def test_matches_reference_quantlinear_path():
+    """The reference's forward (dequantise to fp16, then F.linear) within one fp16 rounding of each other."""
+    lin = torch.nn.Linear(896, 4864, bias=True).half().to(DEV)
+    q = Int4Linear.from_linear(lin, 128)
+    x = torch.randn(32, 896, device=DEV).half()
+    got = q(x)
+    w = torch.from_numpy(dequantize_int4_ref(q.qweight.cpu().numpy(), q.scales.cpu().numpy(),
+                                             q.zeros.cpu().numpy(), 128, "float16")).half().to(DEV)
+    want = F.linear(x.float(), w.float(), q.bias.float())
+    torch.cuda.synchronize()
+    err = (got.float() - want).abs()
+    assert (err <= 2.0 ** -10 * want.abs() + 1e-4).all(), f"max err {err.max().item():.3e}"
+
+
+def test_quantize_model_replaces_linears_and_stays_close():
+    torch.manual_seed(0)
+    m = torch.nn.Sequential(torch.nn.Linear(256, 256, bias=False), torch.nn.SiLU(),
+                            torch.nn.Linear(256, 256, bias=False)).half().to(DEV)
+    x = torch.randn(4, 256, device=DEV).half()
+    ref = m(x).float()
+    report = quantize_model(m, 128, skip=())
+    assert report["layers_quantized"] == 2 and report["compression"] > 3.4
+    got = m(x).float()
+    torch.cuda.synchronize()
+    cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+    assert cos > 0.98, f"int4 output cosine similarity {cos:.4f}"

@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for n in ("ns_reshape_and_cache", "ns_paged_attention", "ns_paged_attention_workspace_size",
-              "ns_rope_reshape_and_cache",
+              "ns_rope_reshape_and_cache", "ns_int4_linear",
               "ns_error_string", "ns_version"):
         assert n in names
 
@@ -145,3 +145,33 @@ def test_rope_reshape_and_cache_rejects_bad_arguments(over, code):
 def test_rope_reshape_and_cache_zero_tokens_is_a_no_op():
     lib = _lib.load()
     assert lib.ns_rope_reshape_and_cache(*_rope_args(T=0, q=None, k=None)) == _lib.NS_OK
+
+
+def _i4_args(**over):
+    a = dict(out=16, x=16, xs=256, qw=16, sc=16, zp=16, bias=None, M=4, N=64, K=256, gs=128,
+             dt=_lib.NS_DTYPE_F16, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("over,code", [
+    (dict(x=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(qw=None), _lib.NS_ERR_INVALID_ARG),
+    (dict(N=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(dt=_lib.NS_DTYPE_F32), _lib.NS_ERR_UNSUPPORTED),
+    (dict(N=72), _lib.NS_ERR_UNSUPPORTED),                # features not a whole number of 16-row tiles
+    (dict(K=240, xs=240), _lib.NS_ERR_UNSUPPORTED),       # K not a multiple of the group size
+    (dict(gs=48), _lib.NS_ERR_UNSUPPORTED),
+    (dict(xs=250), _lib.NS_ERR_INVALID_ARG),              # row stride not 16-byte aligned
+    (dict(xs=128), _lib.NS_ERR_INVALID_ARG),              # row stride shorter than a row
+    (dict(x=24), _lib.NS_ERR_INVALID_ARG),
+    (dict(out=20), _lib.NS_ERR_INVALID_ARG),
+])
+def test_int4_linear_rejects_bad_arguments(over, code):
+    lib = _lib.load()
+    assert lib.ns_int4_linear(*_i4_args(**over)) == code
+
+
+def test_int4_linear_zero_rows_is_a_no_op():
+    lib = _lib.load()
+    assert lib.ns_int4_linear(*_i4_args(M=0, x=None)) == _lib.NS_OK

@@ -1,0 +1,111 @@
+"""Pins the INT4 oracle (oracle/quant.py) and the product's quantiser.
+
+The checks are the reference's own quant tests (reference
+tests/test_quant.py:46-94) restated against the oracle, plus closed forms that
+do not share its code: weights on the quantisation grid round-trip exactly, a
+per-element loop decodes the packed bytes, and the float64 linear equals
+integer arithmetic on integer inputs.  The product's setup-time quantiser
+(nanoserve_amd/quant.py) must produce the oracle's bytes exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nanoserve_amd.quant import quantize_int4_groupwise
+from oracle.quant import dequantize_int4_ref, int4_linear_ref, quantize_int4_ref
+
+
+def _w(out_f, in_f, seed=0):
+    return np.random.default_rng(seed).standard_normal((out_f, in_f)).astype(np.float32)
+
+
+def test_packing_halves_the_bytes():
+    packed, s, z = quantize_int4_ref(_w(32, 256), 128)
+    assert packed.dtype == np.uint8 and packed.shape == (32, 128)
+    assert s.shape == (32, 2) and s.dtype == np.float32 and z.shape == (32, 2) and z.dtype == np.uint8
+
+
+def test_nibbles_unpack_in_the_right_order():
+    w = _w(4, 128, 1)
+    packed, s, z = quantize_int4_ref(w, 128)
+    q = np.clip(np.round(w / s[:, :1]) + z[:, :1], 0, 15).astype(np.uint8)
+    assert np.array_equal(packed & 0x0F, q[:, 0::2])
+    assert np.array_equal(packed >> 4, q[:, 1::2])
+
+
+def test_roundtrip_error_is_bounded_by_the_group_step():
+    w = _w(16, 256, 2)
+    packed, s, z = quantize_int4_ref(w, 128)
+    deq = dequantize_int4_ref(packed, s, z, 128)
+    assert (np.abs(deq - w) <= np.repeat(s, 128, axis=1) * 0.51 + 1e-6).all()
+
+
+def test_grouping_beats_per_tensor_on_outliers():
+    w = _w(8, 256, 3) * 0.01
+    w[:, 0] = 50.0
+    fine = dequantize_int4_ref(*quantize_int4_ref(w, 128), 128)
+    coarse = dequantize_int4_ref(*quantize_int4_ref(w, 256), 256)
+    assert np.abs(fine[:, 1:] - w[:, 1:]).mean() < np.abs(coarse[:, 1:] - w[:, 1:]).mean()
+
+
+def test_bad_group_size_is_rejected():
+    with pytest.raises(ValueError):
+        quantize_int4_ref(_w(4, 100), 128)
+    with pytest.raises(ValueError):
+        quantize_int4_groupwise(torch.randn(4, 100), 128)
+
+
+def test_grid_weights_roundtrip_exactly():
+    """w = (q - z) * s with every group spanning codes 0..15 is reproduced bit for bit."""
+    rng = np.random.default_rng(4)
+    N, K, gs = 6, 256, 128
+    q = rng.integers(0, 16, (N, K))
+    q[:, 0], q[:, 1], q[:, 128], q[:, 129] = 0, 15, 0, 15
+    z = rng.integers(0, 16, (N, K // gs))
+    s = 2.0 ** rng.integers(-8, 0, (N, K // gs))
+    w = ((q - np.repeat(z, gs, axis=1)) * np.repeat(s, gs, axis=1)).astype(np.float32)
+    packed, s2, z2 = quantize_int4_ref(w, gs)
+    assert np.array_equal(s2, s.astype(np.float32)) and np.array_equal(z2, z)
+    assert np.array_equal(dequantize_int4_ref(packed, s2, z2, gs), w)
+
+
+def test_dequantizer_matches_a_per_element_loop():
+    packed, s, z = quantize_int4_ref(_w(3, 256, 5), 128)
+    deq = dequantize_int4_ref(packed, s, z, 128)
+    for n in range(3):
+        for k in range(256):
+            b = int(packed[n, k // 2])
+            code = (b & 15) if k % 2 == 0 else (b >> 4)
+            want = np.float32(np.float32(code - int(z[n, k // 128])) * s[n, k // 128])
+            assert deq[n, k] == want
+
+
+def test_dequantizer_rounds_to_the_model_dtype():
+    packed, s, z = quantize_int4_ref(_w(8, 256, 6), 128)
+    f32 = dequantize_int4_ref(packed, s, z, 128)
+    assert np.array_equal(dequantize_int4_ref(packed, s, z, 128, "float16"), f32.astype(np.float16).astype(np.float32))
+    want = torch.from_numpy(f32).to(torch.bfloat16).float().numpy()
+    assert np.array_equal(dequantize_int4_ref(packed, s, z, 128, "bfloat16"), want)
+
+
+def test_linear_matches_integer_arithmetic():
+    rng = np.random.default_rng(7)
+    x = rng.integers(-8, 9, (5, 64))
+    w = rng.integers(-8, 9, (12, 64))
+    b = rng.integers(-100, 101, 12)
+    y = int4_linear_ref(x.astype(np.float32), w.astype(np.float32), b.astype(np.float32))
+    assert np.array_equal(y, (x @ w.T + b).astype(np.float64))
+
+
+@pytest.mark.parametrize("shape,gs", [((64, 256), 128), ((1152, 896), 128), ((40, 512), 64)])
+def test_product_quantizer_equals_oracle(shape, gs):
+    w = _w(*shape, seed=8) * 0.05
+    w[0, :gs] = 0.0                     # a constant group: scale clamps to 1e-8
+    packed, s, z = quantize_int4_groupwise(torch.from_numpy(w), gs)
+    rp, rs, rz = quantize_int4_ref(w, gs)
+    assert np.array_equal(packed.numpy(), rp)
+    assert np.array_equal(s.numpy(), rs)
+    assert np.array_equal(z.numpy(), rz)
