@@ -1,0 +1,423 @@
+"""A minimal continuous-batching engine around the HIP path.
+
+Enough of the reference engine (nanoserve/engine.py, scheduler.py,
+sequence.py, model_runner.py, metrics.py) to run the end-to-end serving
+benchmark with the kernels inside the model: requests join and leave the
+batch every step, prefill and decode share one token budget, long prompts are
+prefilled in chunks, and when blocks run out the newest running sequence is
+preempted and later recomputed.  Sampling is greedy (the benchmark's setting).
+
+The scheduling rules follow the reference:
+  * running sequences are served first, oldest first, then waiting requests
+    are admitted while budget, sequence slots and blocks last
+    (scheduler.py:91-202);
+  * a sequence that cannot get blocks evicts the newest running sequence not
+    yet granted tokens this step (scheduler.py:204-262);
+  * a step's metadata is built in scheduler order with int64 indices in one
+    host-to-device copy (model_runner.py:52-147); a sequence yields a token
+    only in the step that computes its last uncomputed token.
+"""
+
+from __future__ import annotations
+
+import enum
+import time
+from collections import deque
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from .attention import AttentionMetadata, get_attention_backend
+from .block_manager import BlockSpaceManager
+from .kv_cache import PagedKVCache
+
+
+@dataclass
+class SamplingParams:
+    max_new_tokens: int = 16
+    ignore_eos: bool = False
+
+
+@dataclass
+class SchedulerConfig:
+    max_num_batched_tokens: int = 2048
+    max_num_seqs: int = 64
+    enable_chunked_prefill: bool = True
+
+
+class SeqStatus(enum.Enum):
+    WAITING = enum.auto()
+    RUNNING = enum.auto()
+    PREEMPTED = enum.auto()
+    FINISHED_LENGTH = enum.auto()
+    FINISHED_EOS = enum.auto()
+
+    @property
+    def finished(self) -> bool:
+        return self in (SeqStatus.FINISHED_LENGTH, SeqStatus.FINISHED_EOS)
+
+
+@dataclass
+class RequestMetrics:
+    """Per-request timestamps (reference metrics.py:10-38)."""
+
+    request_id: int
+    prompt_tokens: int
+    arrival: float
+    start: float = 0.0
+    first_token: float = 0.0
+    end: float = 0.0
+    output_tokens: int = 0
+
+    @property
+    def ttft(self) -> float:
+        return self.first_token - self.arrival
+
+    @property
+    def e2e(self) -> float:
+        return self.end - self.arrival
+
+    @property
+    def tpot(self) -> float:
+        """Mean seconds per output token after the first."""
+        if self.output_tokens <= 1:
+            return 0.0
+        return (self.end - self.first_token) / (self.output_tokens - 1)
+
+
+@dataclass(eq=False)
+class Sequence:
+    """One request's state; num_computed_tokens marks how much of it has KV in the cache."""
+
+    seq_id: int
+    prompt_token_ids: list[int]
+    sampling: SamplingParams
+    arrival: float = field(default_factory=time.perf_counter)
+    output_token_ids: list[int] = field(default_factory=list)
+    status: SeqStatus = SeqStatus.WAITING
+    block_table: list[int] = field(default_factory=list)
+    num_computed_tokens: int = 0
+    num_preemptions: int = 0
+    metrics: RequestMetrics | None = None
+
+    def __post_init__(self) -> None:
+        if self.metrics is None:
+            self.metrics = RequestMetrics(self.seq_id, len(self.prompt_token_ids), self.arrival)
+
+    @property
+    def prompt_len(self) -> int:
+        return len(self.prompt_token_ids)
+
+    @property
+    def num_tokens(self) -> int:
+        return len(self.prompt_token_ids) + len(self.output_token_ids)
+
+    @property
+    def num_uncomputed_tokens(self) -> int:
+        return self.num_tokens - self.num_computed_tokens
+
+    @property
+    def is_prefilling(self) -> bool:
+        return self.num_computed_tokens < self.prompt_len
+
+    def slice_token_ids(self, start: int, end: int) -> list[int]:
+        p = self.prompt_len
+        if end <= p:
+            return self.prompt_token_ids[start:end]
+        return (self.prompt_token_ids + self.output_token_ids)[start:end]
+
+    def advance_computed(self, n: int) -> None:
+        self.num_computed_tokens += n
+        assert self.num_computed_tokens <= self.num_tokens
+
+    def reset_for_recompute(self) -> None:
+        self.block_table = []
+        self.num_computed_tokens = 0
+        self.status = SeqStatus.PREEMPTED
+        self.num_preemptions += 1
+
+    def check_stop(self, eos_token_id: int | None) -> bool:
+        if len(self.output_token_ids) >= self.sampling.max_new_tokens:
+            self.status = SeqStatus.FINISHED_LENGTH
+            return True
+        if (not self.sampling.ignore_eos and eos_token_id is not None and self.output_token_ids
+                and self.output_token_ids[-1] == eos_token_id):
+            self.status = SeqStatus.FINISHED_EOS
+            return True
+        return False
+
+
+@dataclass
+class SchedulerOutput:
+    scheduled: list = field(default_factory=list)  # [(Sequence, num_tokens)]
+    preempted: list = field(default_factory=list)
+
+    def __bool__(self) -> bool:
+        return bool(self.scheduled)
+
+
+class Scheduler:
+    def __init__(self, cfg: SchedulerConfig, block_manager: BlockSpaceManager) -> None:
+        self.cfg = cfg
+        self.block_manager = block_manager
+        self.waiting: deque[Sequence] = deque()
+        self.running: list[Sequence] = []
+        self.num_preemptions = 0
+
+    def add(self, seq: Sequence) -> None:
+        seq.status = SeqStatus.WAITING
+        self.waiting.append(seq)
+
+    @property
+    def has_work(self) -> bool:
+        return bool(self.waiting or self.running)
+
+    def schedule(self) -> SchedulerOutput:
+        out = SchedulerOutput()
+        budget = self._schedule_running(out, self.cfg.max_num_batched_tokens)
+        self._schedule_waiting(out, budget)
+        return out
+
+    def _schedule_running(self, out: SchedulerOutput, budget: int) -> int:
+        snapshot = list(self.running)
+        still_running: list[Sequence] = []
+        protected: set[int] = set()
+        for seq in snapshot:
+            if seq.status is not SeqStatus.RUNNING:
+                continue  # evicted earlier in this step
+            if budget <= 0:
+                still_running.append(seq)
+                continue
+            want = min(seq.num_uncomputed_tokens, budget)
+            if not self.cfg.enable_chunked_prefill and seq.is_prefilling:
+                want = seq.num_uncomputed_tokens
+                if want > budget:
+                    still_running.append(seq)
+                    continue
+            need = seq.num_computed_tokens + want
+            admitted = True
+            while not self.block_manager.allocate(seq, need):
+                victim = next((s for s in reversed(snapshot)
+                               if s.status is SeqStatus.RUNNING and s.seq_id not in protected and s is not seq),
+                              None)
+                if victim is None:
+                    cap = self.block_manager.num_total_blocks - self.block_manager.watermark_blocks
+                    if self.block_manager.blocks_for(need) > cap:
+                        raise ValueError(f"request {seq.seq_id} needs {self.block_manager.blocks_for(need)} "
+                                         f"KV blocks but the cache holds {cap}")
+                    # Last one standing: it goes back to the queue and retries.
+                    self._preempt(seq, out)
+                    admitted = False
+                    break
+                self._preempt(victim, out)
+                if victim in still_running:
+                    still_running.remove(victim)
+            if admitted:
+                out.scheduled.append((seq, want))
+                protected.add(seq.seq_id)
+                budget -= want
+                still_running.append(seq)
+        self.running = still_running
+        return budget
+
+    def _schedule_waiting(self, out: SchedulerOutput, budget: int) -> int:
+        just_preempted = {s.seq_id for s in out.preempted}
+        while self.waiting and budget > 0 and len(self.running) < self.cfg.max_num_seqs:
+            seq = self.waiting[0]
+            if seq.seq_id in just_preempted:
+                break
+            want = min(seq.num_uncomputed_tokens, budget)
+            if not self.cfg.enable_chunked_prefill:
+                want = seq.num_uncomputed_tokens
+                if want > self.cfg.max_num_batched_tokens:
+                    raise ValueError(f"prompt of {want} tokens exceeds max_num_batched_tokens; "
+                                     "enable chunked prefill")
+                if want > budget:
+                    break
+            need = seq.num_computed_tokens + want
+            if not self.block_manager.can_allocate(seq, need) or not self.block_manager.allocate(seq, need):
+                break
+            self.waiting.popleft()
+            seq.status = SeqStatus.RUNNING
+            if seq.metrics.start == 0.0:
+                seq.metrics.start = time.perf_counter()
+            self.running.append(seq)
+            out.scheduled.append((seq, want))
+            budget -= want
+        return budget
+
+    def _preempt(self, seq: Sequence, out: SchedulerOutput) -> None:
+        """Newest-first eviction by recompute: free the blocks, requeue at the front."""
+        self.block_manager.free(seq)
+        seq.reset_for_recompute()
+        self.num_preemptions += 1
+        out.preempted.append(seq)
+        self.waiting.appendleft(seq)
+
+    def free_finished(self) -> list[Sequence]:
+        done = [s for s in self.running if s.status.finished]
+        for s in done:
+            self.block_manager.free(s)
+        self.running = [s for s in self.running if not s.status.finished]
+        return done
+
+
+class ModelRunner:
+    """Scheduler decision -> metadata -> forward -> greedy tokens."""
+
+    def __init__(self, model, kv_cache: PagedKVCache, block_manager: BlockSpaceManager, device,
+                 backend: str = "auto") -> None:
+        self.model = model
+        self.kv_cache = kv_cache
+        self.block_manager = block_manager
+        self.device = torch.device(device)
+        self.block_size = kv_cache.block_size
+        self.attn_fn, self.backend_name = get_attention_backend(backend)
+        self._host: torch.Tensor | None = None
+        self._dev: torch.Tensor | None = None
+
+    def _stage(self, chunks: list[list[int]]) -> list[torch.Tensor]:
+        """All integer vectors in one pinned host buffer and one copy (model_runner.py:52-83)."""
+        sizes = [len(c) for c in chunks]
+        total = sum(sizes)
+        if self._host is None or self._host.numel() < total:
+            n = max(2 * total, 8192)
+            self._host = torch.empty(n, dtype=torch.int64, pin_memory=self.device.type == "cuda")
+            self._dev = torch.empty(n, dtype=torch.int64, device=self.device)
+        flat = np.fromiter((v for c in chunks for v in c), dtype=np.int64, count=total)
+        self._host[:total].copy_(torch.from_numpy(flat))
+        self._dev[:total].copy_(self._host[:total])  # blocking: the buffer is reused next step
+        views, off = [], 0
+        for n in sizes:
+            views.append(self._dev[off:off + n])
+            off += n
+        return views
+
+    def build_inputs(self, scheduled):
+        """(input_ids, positions, md, sample_indices or None, sample_seqs) for one step."""
+        input_ids, positions, slots, seq_lens, query_lens = [], [], [], [], []
+        qsl = [0]
+        sample_indices, sample_seqs = [], []
+        for seq, q in scheduled:
+            start, end = seq.num_computed_tokens, seq.num_computed_tokens + q
+            input_ids.extend(seq.slice_token_ids(start, end))
+            positions.extend(range(start, end))
+            slots.extend(self.block_manager.slot_mapping(seq, start, end))
+            qsl.append(qsl[-1] + q)
+            seq_lens.append(end)
+            query_lens.append(q)
+            if end == seq.num_tokens:
+                sample_indices.append(qsl[-1] - 1)
+                sample_seqs.append(seq)
+        max_seq_len = max(seq_lens)
+        max_blocks = -(-max_seq_len // self.block_size)
+        bt: list[int] = []
+        for seq, _ in scheduled:
+            row = seq.block_table[:max_blocks]
+            bt.extend(row)
+            bt.extend([0] * (max_blocks - len(row)))
+        ids_t, pos_t, slot_t, qsl_t, sl_t, bt_t, samp_t = self._stage(
+            [input_ids, positions, slots, qsl, seq_lens, bt, sample_indices])
+        md = AttentionMetadata(
+            slot_mapping=slot_t, query_start_loc=qsl_t, seq_lens=sl_t,
+            block_tables=bt_t.view(len(scheduled), max_blocks),
+            max_query_len=max(query_lens), max_seq_len=max_seq_len,
+            num_seqs=len(scheduled), num_tokens=len(input_ids),
+            is_decode_only=all(q == 1 for q in query_lens),
+            query_lens_cpu=query_lens, seq_lens_cpu=seq_lens, query_start_loc_cpu=qsl)
+        return ids_t, pos_t, md, (samp_t if sample_indices else None), sample_seqs
+
+    @torch.inference_mode()
+    def execute(self, scheduled) -> list[tuple[Sequence, int]]:
+        ids, pos, md, sample_idx, sample_seqs = self.build_inputs(scheduled)
+        hidden = self.model(ids, pos, self.kv_cache, md, self.attn_fn)
+        for seq, q in scheduled:
+            seq.advance_computed(q)
+        if sample_idx is None:
+            return []
+        logits = self.model.compute_logits(hidden, sample_idx)
+        tokens = logits.argmax(dim=-1).tolist()  # greedy; the step's one device-to-host sync
+        return list(zip(sample_seqs, tokens))
+
+
+class LLMEngine:
+    """add_request / step / run_all over a model, a paged cache and the scheduler."""
+
+    def __init__(self, model, num_blocks: int, block_size: int = 16, device="cuda",
+                 scheduler_config: SchedulerConfig | None = None, eos_token_id: int | None = None,
+                 max_model_len: int = 4096) -> None:
+        self.model = model.eval().requires_grad_(False)
+        self.device = torch.device(device)
+        dtype = model.model.embed_tokens.weight.dtype
+        self.kv_cache = PagedKVCache(num_blocks, block_size, model.num_layers, model.num_kv_heads,
+                                     model.head_dim, dtype, device)
+        self.block_manager = BlockSpaceManager(block_size, num_blocks, watermark=0.0)
+        self.scheduler = Scheduler(scheduler_config or SchedulerConfig(), self.block_manager)
+        self.runner = ModelRunner(model, self.kv_cache, self.block_manager, device)
+        self.eos_token_id = eos_token_id
+        self.max_model_len = max_model_len
+        self._next_id = 0
+        self.finished: list[Sequence] = []
+
+    def add_request(self, prompt_token_ids: list[int], sampling: SamplingParams | None = None) -> int:
+        sampling = sampling or SamplingParams()
+        if len(prompt_token_ids) + sampling.max_new_tokens > self.max_model_len:
+            raise ValueError("request exceeds max_model_len")
+        seq = Sequence(self._next_id, list(prompt_token_ids), sampling)
+        self._next_id += 1
+        self.scheduler.add(seq)
+        return seq.seq_id
+
+    @property
+    def has_unfinished_requests(self) -> bool:
+        return self.scheduler.has_work
+
+    def step(self) -> list[Sequence]:
+        sched = self.scheduler.schedule()
+        if not sched:
+            return []
+        results = self.runner.execute(sched.scheduled)
+        now = time.perf_counter()
+        for seq, tok in results:
+            seq.output_token_ids.append(tok)
+            m = seq.metrics
+            if m.first_token == 0.0:
+                m.first_token = now
+            m.output_tokens = len(seq.output_token_ids)
+            m.end = now
+            seq.check_stop(self.eos_token_id)
+        done = self.scheduler.free_finished()
+        self.finished.extend(done)
+        return done
+
+    def run_all(self) -> list[Sequence]:
+        out: list[Sequence] = []
+        while self.has_unfinished_requests:
+            out.extend(self.step())
+        return sorted(out, key=lambda s: s.seq_id)
+
+
+def summarize(records: list[RequestMetrics], wall_time: float) -> dict:
+    """Throughput over wall time and TTFT/TPOT/E2E percentiles (reference metrics.py:45-78)."""
+    def pct(v, q):
+        return float(np.percentile(v, q)) if len(v) else 0.0
+
+    ttft = [r.ttft * 1e3 for r in records]
+    tpot = [r.tpot * 1e3 for r in records if r.output_tokens > 1]
+    e2e = [r.e2e * 1e3 for r in records]
+    out_tok = sum(r.output_tokens for r in records)
+    in_tok = sum(r.prompt_tokens for r in records)
+    res = {
+        "num_requests": len(records),
+        "wall_time_s": wall_time,
+        "prompt_tokens": in_tok,
+        "output_tokens": out_tok,
+        "output_tok_per_s": out_tok / wall_time if wall_time else 0.0,
+        "total_tok_per_s": (in_tok + out_tok) / wall_time if wall_time else 0.0,
+    }
+    for name, v in (("ttft", ttft), ("tpot", tpot), ("e2e", e2e)):
+        res[f"{name}_mean_ms"] = float(np.mean(v)) if v else 0.0
+        for q in (50, 90, 99):
+            res[f"{name}_p{q}_ms"] = pct(v, q)
+    return res

@@ -1,0 +1,183 @@
+"""The engine harness on the GPU: the Qwen2 forward with every HIP kernel inside.
+
+The model runs INT4 projections (ns_int4_linear), the fused rotary + cache
+write (ns_rope_reshape_and_cache) and paged attention (ns_paged_attention);
+the oracle (oracle/qwen2.py, pinned against transformers on the CPU) runs the
+reference forward in float32.  Bounds: logits within 1e-2 of the oracle's
+(max |diff| / max |oracle|, fp16 activations rounded after every op), and the
+reference's model properties (tests/test_model.py:54-136) within the same
+bound: incremental decode == one-shot prefill, chunked == one-shot, and a
+sequence's logits independent of its batchmates.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from nanoserve_amd.block_manager import BlockSpaceManager
+from nanoserve_amd.engine import LLMEngine, ModelRunner, SamplingParams, SchedulerConfig, Sequence
+from nanoserve_amd.kv_cache import PagedKVCache
+from nanoserve_amd.model import Qwen2Config, Qwen2ForCausalLM, random_init_
+from nanoserve_amd.quant import quantize_model
+from oracle.qwen2 import qwen2_forward_ref, relative_error
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-2
+TINY = dict(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+            num_attention_heads=4, num_key_value_heads=2, rope_theta=10000.0, tie_word_embeddings=False)
+
+
+def _model(cfg_kw=TINY, dtype=torch.float16, int4=True, fuse=True, seed=0, std=0.05):
+    m = random_init_(Qwen2ForCausalLM(Qwen2Config(**cfg_kw), max_position=2048), std=std, seed=seed)
+    m = m.to(dtype).to(DEV)
+    if int4:
+        quantize_model(m, 128)
+    if fuse:
+        m.fuse_projections()
+    return m.eval().requires_grad_(False)
+
+
+def _runner(model, num_blocks=64, block_size=8):
+    cache = PagedKVCache(num_blocks, block_size, model.num_layers, model.num_kv_heads, model.head_dim,
+                         model.model.embed_tokens.weight.dtype, DEV)
+    bm = BlockSpaceManager(block_size, num_blocks, watermark=0.0)
+    return ModelRunner(model, cache, bm, DEV), bm
+
+
+def _seq(i, tokens, max_new=4):
+    return Sequence(i, list(tokens), SamplingParams(max_new_tokens=max_new, ignore_eos=True))
+
+
+def _tokens(n, vocab, seed):
+    return torch.randint(0, vocab, (n,), generator=torch.Generator().manual_seed(seed)).tolist()
+
+
+@torch.inference_mode()
+def _step(runner, bm, plan):
+    """Run one forward over plan [(seq, q)]; return (logits of sampled rows, sample_seqs, md, ids, pos)."""
+    for s, q in plan:
+        assert bm.allocate(s, s.num_computed_tokens + q)
+    ids, pos, md, si, seqs = runner.build_inputs(plan)
+    hidden = runner.model(ids, pos, runner.kv_cache, md, runner.attn_fn)
+    logits = runner.model.compute_logits(hidden, si) if si is not None else None
+    for s, q in plan:
+        s.advance_computed(q)
+    return logits, seqs, md, ids, pos
+
+
+@pytest.mark.parametrize("int4,fuse,dtype", [(True, True, torch.float16), (True, False, torch.float16),
+                                             (False, True, torch.float16), (True, True, torch.bfloat16)])
+def test_forward_matches_oracle_on_a_mixed_batch(int4, fuse, dtype):
+    model = _model(int4=int4, fuse=fuse, dtype=dtype)
+    runner, bm = _runner(model)
+    a, b = _seq(0, _tokens(21, 512, 1)), _seq(1, _tokens(9, 512, 2))
+    kc = [t.cpu() for t in runner.kv_cache.k_cache]
+    vc = [t.cpu() for t in runner.kv_cache.v_cache]
+    # Step 1: both prefill; step 2: a decodes while c prefills beside it.
+    logits, seqs, md, ids, pos = _step(runner, bm, [(a, 21), (b, 9)])
+    want, kc, vc = qwen2_forward_ref(model, ids, pos, kc, vc, md, torch.tensor([20, 29]))
+    torch.cuda.synchronize()
+    assert relative_error(logits, want) < (TOL if dtype == torch.float16 else 3 * TOL)
+    a.output_token_ids.append(int(want[0].argmax()))
+    c = _seq(2, _tokens(30, 512, 3))
+    logits, seqs, md, ids, pos = _step(runner, bm, [(a, 1), (c, 30)])
+    want, _, _ = qwen2_forward_ref(model, ids, pos, kc, vc, md, torch.tensor([0, 30]))
+    torch.cuda.synchronize()
+    assert relative_error(logits, want) < (TOL if dtype == torch.float16 else 3 * TOL)
+
+
+def test_qwen_half_billion_shapes_two_layers_match_oracle():
+    cfg = dict(num_hidden_layers=2)  # Qwen2.5-0.5B widths: hidden 896, 14/2 heads, D 64, vocab 151936
+    model = _model(cfg, std=0.02)
+    runner, bm = _runner(model, num_blocks=32, block_size=16)
+    a, b = _seq(0, _tokens(40, 151936, 4)), _seq(1, _tokens(7, 151936, 5))
+    kc = [t.cpu() for t in runner.kv_cache.k_cache]
+    vc = [t.cpu() for t in runner.kv_cache.v_cache]
+    logits, _, md, ids, pos = _step(runner, bm, [(a, 40), (b, 7)])
+    want, _, _ = qwen2_forward_ref(model, ids, pos, kc, vc, md, torch.tensor([39, 46]))
+    torch.cuda.synchronize()
+    assert relative_error(logits, want) < TOL
+
+
+@pytest.mark.parametrize("block_size", [8, 16])
+def test_token_by_token_matches_one_shot_prefill(block_size):
+    model = _model()
+    toks = _tokens(23, 512, 6)
+    r1, bm1 = _runner(model, block_size=block_size)
+    whole, *_ = _step(r1, bm1, [(_seq(0, toks), 23)])
+    r2, bm2 = _runner(model, block_size=block_size)
+    s = _seq(0, toks)
+    for _ in range(23):
+        last, *_ = _step(r2, bm2, [(s, 1)])
+    torch.cuda.synchronize()
+    assert relative_error(last, whole) < TOL
+
+
+def test_chunked_prefill_matches_one_shot():
+    model = _model()
+    toks = _tokens(30, 512, 7)
+    r1, bm1 = _runner(model)
+    whole, *_ = _step(r1, bm1, [(_seq(0, toks), 30)])
+    r2, bm2 = _runner(model)
+    s = _seq(0, toks)
+    for q in (7, 11, 12):
+        last, *_ = _step(r2, bm2, [(s, q)])
+    torch.cuda.synchronize()
+    assert relative_error(last, whole) < TOL
+
+
+def test_logits_are_independent_of_batchmates():
+    model = _model()
+    a_t, b_t = _tokens(12, 512, 8), _tokens(25, 512, 9)
+    r1, bm1 = _runner(model)
+    alone, *_ = _step(r1, bm1, [(_seq(0, a_t), 12)])
+    r2, bm2 = _runner(model)
+    sa, sb = _seq(0, a_t), _seq(1, b_t)
+    together, seqs, *_ = _step(r2, bm2, [(sa, 12), (sb, 25)])
+    torch.cuda.synchronize()
+    assert relative_error(together[seqs.index(sa)][None], alone) < TOL
+
+
+def test_engine_runs_requests_to_completion_deterministically():
+    def run(num_blocks):
+        model = _model(seed=3)
+        eng = LLMEngine(model, num_blocks=num_blocks, block_size=8, device=DEV,
+                        scheduler_config=SchedulerConfig(max_num_batched_tokens=64, max_num_seqs=8),
+                        max_model_len=256)
+        lens = [(5, 6), (33, 3), (17, 9), (70, 4), (2, 12), (40, 7)]
+        for i, (p, n) in enumerate(lens):
+            eng.add_request(_tokens(p, 512, 100 + i), SamplingParams(max_new_tokens=n, ignore_eos=True))
+        out = eng.run_all()
+        assert [len(s.output_token_ids) for s in out] == [n for _, n in lens]
+        assert all(0 <= t < 512 for s in out for t in s.output_token_ids)
+        return [s.output_token_ids for s in out], eng.scheduler.num_preemptions
+
+    toks1, pre1 = run(128)
+    toks2, _ = run(128)
+    assert toks1 == toks2 and pre1 == 0
+    # A cache too small for all requests at once: sequences are preempted and recomputed.
+    _, pre3 = run(16)
+    assert pre3 > 0
+
+
+def test_first_greedy_token_matches_oracle_when_not_a_near_tie():
+    model = _model(seed=4)
+    runner, bm = _runner(model)
+    kc = [t.cpu() for t in runner.kv_cache.k_cache]
+    vc = [t.cpu() for t in runner.kv_cache.v_cache]
+    seqs = [_seq(i, _tokens(5 + 7 * i, 512, 200 + i)) for i in range(4)]
+    for s in seqs:
+        assert bm.allocate(s, s.prompt_len)
+    ids, pos, md, si, order = runner.build_inputs([(s, s.prompt_len) for s in seqs])
+    got = runner.execute([(s, s.prompt_len) for s in seqs])
+    want, _, _ = qwen2_forward_ref(model, ids, pos, kc, vc, md, si)
+    top2 = want.topk(2, dim=-1).values
+    checked = 0
+    for i, (s, tok) in enumerate(got):
+        margin = float(top2[i, 0] - top2[i, 1])
+        if margin > 5 * TOL * float(want.abs().max()):
+            assert tok == int(want[i].argmax())
+            checked += 1
+    assert checked >= 1
