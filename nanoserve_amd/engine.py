@@ -125,7 +125,9 @@ class Sequence:
         p = self.prompt_len
         if end <= p:
             return self.prompt_token_ids[start:end]
-        return (self.prompt_token_ids + self.output_token_ids)[start:end]
+        if start >= p:
+            return self.output_token_ids[start - p:end - p]
+        return self.prompt_token_ids[start:] + self.output_token_ids[:end - p]
 
     def advance_computed(self, n: int) -> None:
         self.num_computed_tokens += n
@@ -264,10 +266,16 @@ class Scheduler:
 
 
 class ModelRunner:
-    """Scheduler decision -> metadata -> forward -> greedy tokens."""
+    """Scheduler decision -> metadata -> forward -> greedy tokens.
+
+    With `use_graphs`, decode-only steps replay a HIP graph of the whole
+    forward (embedding to greedy token) captured once per batch-size bucket;
+    other steps run eagerly.  See `DecodeGraphs`.
+    """
 
     def __init__(self, model, kv_cache: PagedKVCache, block_manager: BlockSpaceManager, device,
-                 backend: str = "auto") -> None:
+                 backend: str = "auto", use_graphs: bool = False, max_model_len: int = 4096,
+                 graph_batch_sizes: tuple[int, ...] = (1, 2, 4, 8, 16, 24, 32, 48, 64)) -> None:
         self.model = model
         self.kv_cache = kv_cache
         self.block_manager = block_manager
@@ -276,6 +284,7 @@ class ModelRunner:
         self.attn_fn, self.backend_name = get_attention_backend(backend)
         self._host: torch.Tensor | None = None
         self._dev: torch.Tensor | None = None
+        self.graphs = DecodeGraphs(self, graph_batch_sizes, max_model_len) if use_graphs else None
 
     def _stage(self, chunks: list[list[int]]) -> list[torch.Tensor]:
         """All integer vectors in one pinned host buffer and one copy (model_runner.py:52-83)."""
@@ -330,6 +339,8 @@ class ModelRunner:
 
     @torch.inference_mode()
     def execute(self, scheduled) -> list[tuple[Sequence, int]]:
+        if self.graphs is not None and self.graphs.covers(scheduled):
+            return self.graphs.execute(scheduled)
         ids, pos, md, sample_idx, sample_seqs = self.build_inputs(scheduled)
         hidden = self.model(ids, pos, self.kv_cache, md, self.attn_fn)
         for seq, q in scheduled:
@@ -341,12 +352,123 @@ class ModelRunner:
         return list(zip(sample_seqs, tokens))
 
 
+class DecodeGraphs:
+    """HIP graphs of the decode step, one per batch-size bucket.
+
+    A decode step is ~12 launches per layer plus the logits; replaying a
+    captured graph removes the per-launch host cost, which dominates at
+    Qwen2.5-0.5B size.  Each graph reads its inputs from one static int64
+    device buffer (token ids, positions, slots, lengths, block tables) that
+    is refilled by a single host-to-device copy before the replay, and leaves
+    the greedy tokens in a static output.  Batches are padded to the bucket
+    with slot -1 (the cache write skips it) and length 1.
+
+    Attention inside the graph gets no host lengths, so it runs its full-grid
+    decode (splits sized for max_model_len, empty splits exit at once); the
+    block tables have max_model_len / block_size columns.
+    """
+
+    def __init__(self, runner: "ModelRunner", sizes: tuple[int, ...], max_model_len: int) -> None:
+        self.runner = runner
+        self.sizes = sorted(sizes)
+        self.max_model_len = max_model_len
+        self.width = -(-max_model_len // runner.block_size)
+        n = max(self.sizes)
+        self._per = 4 * n + n * self.width  # ids, pos, slots, lens, tables
+        self._host = torch.empty(self._per, dtype=torch.int64, pin_memory=runner.device.type == "cuda")
+        self._dev = torch.zeros(self._per, dtype=torch.int64, device=runner.device)
+        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        self.last_logits: torch.Tensor | None = None  # graph-owned logits of the latest replay
+        self._pool = None
+        self._stream = torch.cuda.Stream(runner.device) if runner.device.type == "cuda" else None
+
+    def covers(self, scheduled) -> bool:
+        return (len(scheduled) <= self.sizes[-1] and all(q == 1 for _, q in scheduled)
+                and all(s.num_tokens <= self.max_model_len for s, _ in scheduled))
+
+    def _views(self, b: int):
+        n = max(self.sizes)
+        d = self._dev
+        return (d[0:b], d[n:n + b], d[2 * n:2 * n + b], d[3 * n:3 * n + b],
+                d[4 * n:4 * n + b * self.width].view(b, self.width))
+
+    def _metadata(self, b: int) -> tuple[torch.Tensor, torch.Tensor, AttentionMetadata]:
+        ids, pos, slots, lens, tables = self._views(b)
+        md = AttentionMetadata(
+            slot_mapping=slots, query_start_loc=None, seq_lens=lens, block_tables=tables,
+            max_query_len=1, max_seq_len=self.max_model_len, num_seqs=b, num_tokens=b,
+            is_decode_only=True, query_lens_cpu=None, seq_lens_cpu=None, query_start_loc_cpu=None)
+        return ids, pos, md
+
+    def _fill(self, scheduled, b: int) -> None:
+        n = max(self.sizes)
+        h = np.zeros(self._per, dtype=np.int64)
+        h[2 * n:2 * n + b] = -1  # padding rows write no cache slot
+        h[3 * n:3 * n + b] = 1
+        bs, w = self.runner.block_size, self.width
+        for i, (seq, _) in enumerate(scheduled):
+            p = seq.num_computed_tokens
+            h[i] = seq.slice_token_ids(p, p + 1)[0]
+            h[n + i] = p
+            h[2 * n + i] = seq.block_table[p // bs] * bs + p % bs
+            h[3 * n + i] = p + 1
+            row = seq.block_table[:w]
+            h[4 * n + i * w:4 * n + i * w + len(row)] = row
+        self._host.copy_(torch.from_numpy(h))
+        self._dev.copy_(self._host)  # ordered before the replay on the same stream
+
+    def _capture(self, b: int):
+        r = self.runner
+        ids, pos, md = self._metadata(b)
+
+        def forward():
+            hidden = r.model(ids, pos, r.kv_cache, md, r.attn_fn)
+            logits = r.model.compute_logits(hidden)
+            return logits.argmax(dim=-1), logits
+
+        s = self._stream
+        s.wait_stream(torch.cuda.current_stream(r.device))
+        with torch.cuda.stream(s):  # warm-up: workspaces and allocator state for this stream
+            forward()
+            forward()
+        s.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, pool=self._pool, stream=s):
+            out, logits = forward()
+        if self._pool is None:
+            self._pool = g.pool()
+        self._graphs[b] = (g, out, logits)
+
+    def capture_all(self) -> None:
+        """Capture every bucket up front, largest first (the pool then fits the rest)."""
+        self._dev.zero_()
+        self._dev[3 * max(self.sizes):4 * max(self.sizes)] = 1
+        self._dev[2 * max(self.sizes):3 * max(self.sizes)] = -1
+        for b in sorted(self.sizes, reverse=True):
+            if b not in self._graphs:
+                self._capture(b)
+
+    def execute(self, scheduled) -> list[tuple[Sequence, int]]:
+        r = self.runner
+        b = next(x for x in self.sizes if x >= len(scheduled))
+        if b not in self._graphs:
+            self.capture_all()
+        g, out, logits = self._graphs[b]
+        self._fill(scheduled, b)
+        g.replay()
+        self.last_logits = logits[:len(scheduled)]
+        tokens = out[:len(scheduled)].tolist()
+        for seq, q in scheduled:
+            seq.advance_computed(q)
+        return [(seq, tok) for (seq, _), tok in zip(scheduled, tokens)]
+
+
 class LLMEngine:
     """add_request / step / run_all over a model, a paged cache and the scheduler."""
 
     def __init__(self, model, num_blocks: int, block_size: int = 16, device="cuda",
                  scheduler_config: SchedulerConfig | None = None, eos_token_id: int | None = None,
-                 max_model_len: int = 4096) -> None:
+                 max_model_len: int = 4096, use_graphs: bool = False) -> None:
         self.model = model.eval().requires_grad_(False)
         self.device = torch.device(device)
         dtype = model.model.embed_tokens.weight.dtype
@@ -354,7 +476,8 @@ class LLMEngine:
                                      model.head_dim, dtype, device)
         self.block_manager = BlockSpaceManager(block_size, num_blocks, watermark=0.0)
         self.scheduler = Scheduler(scheduler_config or SchedulerConfig(), self.block_manager)
-        self.runner = ModelRunner(model, self.kv_cache, self.block_manager, device)
+        self.runner = ModelRunner(model, self.kv_cache, self.block_manager, device,
+                                  use_graphs=use_graphs, max_model_len=max_model_len)
         self.eos_token_id = eos_token_id
         self.max_model_len = max_model_len
         self._next_id = 0
