@@ -46,6 +46,11 @@ extern "C" {
 #define NS_DTYPE_F16 1
 #define NS_DTYPE_BF16 2
 
+/* Epilogues of ns_int4_linear. */
+#define NS_EPILOGUE_NONE 0
+#define NS_EPILOGUE_RESIDUAL 1
+#define NS_EPILOGUE_SILU_MUL 2
+
 /* Human-readable text for a status code (static storage, never NULL). */
 const char* ns_error_string(int code);
 
@@ -122,14 +127,35 @@ int ns_rope_reshape_and_cache(void* q_out, const void* query,
  *   scales  [N, K/group_size] float32;  zeros [N, K/group_size] uint8;
  *   w(n, k) = (code - zero) * scale in float32, rounded to `dtype`.
  * x is [M, K] with row stride x_stride_row (elements, a multiple of 8, rows
- * 16-byte aligned); out is [M, N] contiguous (8-byte aligned); bias is [N]
- * in `dtype` or NULL.  Accumulation is fp32 (MFMA); out = round(acc + bias).
+ * 16-byte aligned); bias is [N] in `dtype` or NULL.  Accumulation is fp32
+ * (MFMA); y = round(acc + bias) is what F.linear returns.  The epilogue then
+ * continues the reference's next elementwise op in the same launch, rounding
+ * where the reference's separate tensor ops round:
+ *   NS_EPILOGUE_NONE      out [M, N] = y;
+ *   NS_EPILOGUE_RESIDUAL  out [M, N] = round(y + residual), residual [M, N]
+ *                         contiguous (may be out itself): the residual add
+ *                         after o_proj / down_proj (reference qwen2.py:78-84);
+ *   NS_EPILOGUE_SILU_MUL  W's rows are interleaved (gate_j, up_j) pairs and
+ *                         out [M, N/2] = round(round(silu(gate)) * up): the
+ *                         SwiGLU of reference layers.py:108-109.
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16.  N must be a multiple of 16, K and
- * group_size multiples of 32 with K a multiple of group_size.
+ * group_size multiples of 32 with K a multiple of group_size; qweight 16-byte
+ * aligned, out 8-byte aligned.
  */
 int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                    const void* qweight, const void* scales, const void* zeros, const void* bias,
+                   const void* residual, int epilogue,
                    int64_t M, int N, int K, int group_size, int dtype, void* stream);
+
+/*
+ * ns_argmax_rows -- out[m] = index of the largest element of row m of x
+ * ([M, N] with row stride x_stride_row elements), the first such index on
+ * ties and the first NaN if the row holds one: torch.argmax(dim=-1), which
+ * the reference's greedy sampler calls (nanoserve/sampler.py:24-27).  out is
+ * int64.  dtype is NS_DTYPE_F32, NS_DTYPE_F16 or NS_DTYPE_BF16.
+ */
+int ns_argmax_rows(int64_t* out, const void* x, int64_t x_stride_row, int64_t M, int64_t N,
+                   int dtype, void* stream);
 
 /*
  * ns_paged_attention_workspace_size -- bytes of device workspace that

@@ -29,6 +29,10 @@ NS_DTYPE_F32 = 0
 NS_DTYPE_F16 = 1
 NS_DTYPE_BF16 = 2
 
+NS_EPILOGUE_NONE = 0
+NS_EPILOGUE_RESIDUAL = 1
+NS_EPILOGUE_SILU_MUL = 2
+
 DTYPE_CODES = {
     torch.float32: NS_DTYPE_F32,
     torch.float16: NS_DTYPE_F16,
@@ -61,8 +65,13 @@ SIGNATURES = {
     "ns_int4_linear": (c_int, [
         c_void_p, c_void_p, c_int64,             # out, x, x row stride
         c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)
+        c_void_p, c_int,                         # residual (or None), epilogue
         c_int64, c_int, c_int, c_int,            # M, N, K, group_size
         c_int, c_void_p,                         # dtype, stream
+    ]),
+    "ns_argmax_rows": (c_int, [
+        c_void_p, c_void_p, c_int64,             # out (int64), x, x row stride
+        c_int64, c_int64, c_int, c_void_p,       # M, N, dtype, stream
     ]),
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,

@@ -16,25 +16,29 @@
 // MFMA sees the reference's own dequantised weights.
 //
 // Tiling (gfx950, wave64): a workgroup owns 16 output features (one MFMA row
-// tile of W) and MT tokens (MT/16 MFMA column tiles of x^T).  Its four waves
-// split K into four contiguous ranges and reduce through LDS.  Per 32-wide K
-// step a lane loads 4 bytes of packed weights (row n0 + lane%16, codes
-// 8·(lane/16) .. +7 of the step: exactly its MFMA A operand) and one 16-byte
-// row piece of x per column tile (its B operand).  The result D[n][m] lands as
-// four consecutive features of one token per lane: one 8-byte store.
+// tile of W) and MT tokens (MT/16 MFMA column tiles of x^T).  K is walked in
+// chunks of 128; the workgroup's WAVES waves split the chunks between them
+// and reduce through LDS.  Within a chunk, lane group g = lane/16 owns the 32
+// consecutive k values [128c + 32g, +32) of its feature row: one 16-byte load
+// brings all 32 codes, which feed four MFMA steps (k order permuted the same
+// way for both operands, so the sum is unchanged).  The same lane reads the
+// matching 8 x values per step for each column tile.  The result D[n][m]
+// lands as four consecutive features of one token per lane: one 8-byte store.
 #include "ns_common.h"
 
 namespace ns {
 namespace {
 
 struct Int4LinearParams {
-  void* out;              // [M, N] contiguous, model dtype
+  void* out;              // [M, N] contiguous ([M, N/2] for NS_EPILOGUE_SILU_MUL), model dtype
   const char* x;          // [M, K] rows of x_stride elements
   int64_t x_stride;
   const uint8_t* qweight; // [N, K/2]
   const float* scales;    // [N, G]
   const uint8_t* zeros;   // [N, G]
   const void* bias;       // [N] model dtype, or null
+  const void* residual;   // [M, N] contiguous, model dtype (NS_EPILOGUE_RESIDUAL)
+  int epilogue;
   int M, N, K, group_size, groups;
 };
 
@@ -48,20 +52,58 @@ __device__ __forceinline__ float from_model(typename DT::T x) {
   return static_cast<float>(x);
 }
 
-template <class DT, int MT>
-__global__ __launch_bounds__(256) void int4_linear_kernel(Int4LinearParams p) {
+// Eight codes (one 32-bit word, even k in the low nibble) -> model-dtype weights.
+template <class DT>
+__device__ __forceinline__ typename DT::vec8 dequant8(uint32_t word, float zero, float scale) {
+  typename DT::vec8 a;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float q = static_cast<float>((word >> (4 * e)) & 0xFu);
+    a[e] = to_model<DT>((q - zero) * scale);
+  }
+  return a;
+}
+
+// SiLU in float32 as torch evaluates it for half tensors: x / (1 + exp(-x)).
+__device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
+
+template <class DT, int MT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParams p) {
   constexpr int NT = MT / 16;  // MFMA column tiles
+  constexpr int ESZ = sizeof(typename DT::T);
+  constexpr int BATCH = 4;     // 128-wide chunks whose weights one wave loads at once
   using V8 = typename DT::vec8;
+  using T = typename DT::T;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * MT;
-  const int row = lane & 15;      // A row (feature) / B column (token) of this lane
-  const int kq = 8 * (lane >> 4); // this lane's 8 k-slots within a K step
+  const int row = lane & 15;  // A row (feature) / B column (token) of this lane
+  const int grp = lane >> 4;  // lane group: k-slots 8*grp .. +7 of an MFMA step
+  const int nf = n0 + 4 * grp; // first of the four output features this lane ends with
 
-  const int steps = p.K / 32;
-  const int s_begin = (steps * wave) / 4;
-  const int s_end = (steps * (wave + 1)) / 4;
+  // The epilogue's inputs are fetched first so their latency hides behind the K loop.
+  float bias[4] = {0.f, 0.f, 0.f, 0.f};
+  float resid[NT][4];
+  if (wave == 0) {
+    if (p.bias) {
+      const T* bp = static_cast<const T*>(p.bias) + nf;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(bp[r]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int m = m0 + 16 * t + row;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) resid[t][r] = 0.f;
+      if (p.epilogue == NS_EPILOGUE_RESIDUAL && m < p.M) {
+        const typename DT::vec4 rv = *reinterpret_cast<const typename DT::vec4*>(
+            static_cast<const T*>(p.residual) + static_cast<int64_t>(m) * p.N + nf);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) resid[t][r] = from_model<DT>(rv[r]);
+      }
+    }
+  }
 
   const int n = n0 + row;
   const uint8_t* wrow = p.qweight + static_cast<int64_t>(n) * (p.K / 2);
@@ -73,34 +115,66 @@ __global__ __launch_bounds__(256) void int4_linear_kernel(Int4LinearParams p) {
   for (int t = 0; t < NT; ++t) {
     const int m = m0 + 16 * t + row;
     xok[t] = m < p.M;
-    xrow[t] = p.x + static_cast<int64_t>(xok[t] ? m : 0) * p.x_stride * sizeof(typename DT::T);
+    xrow[t] = p.x + static_cast<int64_t>(xok[t] ? m : 0) * p.x_stride * ESZ;
   }
 
   floatx4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = s_begin; s < s_end; ++s) {
-    const int k = 32 * s + kq;
-    const uint32_t codes = *reinterpret_cast<const uint32_t*>(wrow + k / 2);
-    const int g = k / p.group_size;
-    const float scale = srow[g];
-    const float zero = static_cast<float>(zrow[g]);
-    V8 a;
+  // Whole 128-wide chunks, split between the waves; each wave fetches the
+  // codes, scales and zeros of up to BATCH chunks before using any of them.
+  const int chunks = p.K / 128;
+  const int c_end = (chunks * (wave + 1)) / WAVES;
+  for (int c0 = (chunks * wave) / WAVES; c0 < c_end; c0 += BATCH) {
+    const int nb = c_end - c0 < BATCH ? c_end - c0 : BATCH;
+    u32x4 codes[BATCH];
+    float scale[BATCH], zero[BATCH];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float q = static_cast<float>((codes >> (4 * e)) & 0xFu);
-      a[e] = to_model<DT>((q - zero) * scale);
+    for (int i = 0; i < BATCH; ++i) {
+      if (i < nb) {
+        const int kb = 128 * (c0 + i) + 32 * grp;
+        codes[i] = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
+        const int gi = kb / p.group_size;
+        scale[i] = srow[gi];
+        zero[i] = static_cast<float>(zrow[gi]);
+      }
     }
 #pragma unroll
+    for (int i = 0; i < BATCH; ++i) {
+      if (i < nb) {
+        const int kb = 128 * (c0 + i) + 32 * grp;
+        V8 b[4][NT];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t)
+            b[j][t] = xok[t] ? load16<DT>(xrow[t] + (kb + 8 * j) * ESZ) : zero8<DT>();
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const V8 a = dequant8<DT>(codes[i][j], zero[i], scale[i]);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+        }
+      }
+    }
+  }
+  // Remaining 32-wide steps when K is not a multiple of 128.
+  for (int s = 4 * chunks + wave; s < p.K / 32; s += WAVES) {
+    const int k = 32 * s + 8 * grp;
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow + k / 2);
+    const int gi = k / p.group_size;
+    const V8 a = dequant8<DT>(word, static_cast<float>(zrow[gi]), srow[gi]);
+#pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const V8 b = xok[t] ? load16<DT>(xrow[t] + k * sizeof(typename DT::T)) : zero8<DT>();
+      const V8 b = xok[t] ? load16<DT>(xrow[t] + k * ESZ) : zero8<DT>();
       acc[t] = mfma16x16x32(DT{}, a, b, acc[t]);
     }
   }
 
-  // Waves 1-3 hand their partial sums to wave 0.
-  __shared__ floatx4 red[3][NT][64];
+  // Waves 1.. hand their partial sums to wave 0.
+  __shared__ floatx4 red[WAVES - 1][NT][64];
   if (wave > 0) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
@@ -110,46 +184,74 @@ __global__ __launch_bounds__(256) void int4_linear_kernel(Int4LinearParams p) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int w = 0; w < 3; ++w) acc[t] += red[w][t][lane];
+    for (int w = 0; w < WAVES - 1; ++w) acc[t] += red[w][t][lane];
   }
 
-  // D[4·(lane/16) + r][lane%16]: features nf .. nf+3 of token m.
-  const int nf = n0 + 4 * (lane >> 4);
-  float bias[4] = {0.f, 0.f, 0.f, 0.f};
-  if (p.bias) {
-    const typename DT::T* b = static_cast<const typename DT::T*>(p.bias) + nf;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(b[r]);
-  }
+  // D[4·(lane/16) + r][lane%16]: features nf .. nf+3 of token m.  Each
+  // epilogue rounds where the reference's separate tensor ops round.
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int m = m0 + 16 * t + row;
     if (m >= p.M) continue;
+    float y[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) y[r] = from_model<DT>(to_model<DT>(acc[t][r] + bias[r]));
+    if (p.epilogue == NS_EPILOGUE_SILU_MUL) {
+      // Rows (nf, nf+1) and (nf+2, nf+3) are (gate, up) pairs of outputs nf/2, nf/2+1.
+      typename DT::T o[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const float act = from_model<DT>(to_model<DT>(silu_f32(y[2 * h])));
+        o[h] = to_model<DT>(act * y[2 * h + 1]);
+      }
+      T* dst = static_cast<T*>(p.out) + static_cast<int64_t>(m) * (p.N / 2) + nf / 2;
+      dst[0] = o[0];
+      dst[1] = o[1];
+      continue;
+    }
     typename DT::vec4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(acc[t][r] + bias[r]);
-    *reinterpret_cast<typename DT::vec4*>(static_cast<typename DT::T*>(p.out) +
-                                          static_cast<int64_t>(m) * p.N + nf) = o;
+    for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + resid[t][r]);
+    *reinterpret_cast<typename DT::vec4*>(static_cast<T*>(p.out) + static_cast<int64_t>(m) * p.N + nf) = o;
   }
+}
+
+// Waves per workgroup: enough that each keeps a few 128-wide chunks in flight
+// for long K (down_proj's 4864 is 38 chunks), within the VGPR budget of the
+// tile: 12 waves (3 per SIMD) for up to 32 tokens, 8 otherwise.
+template <class DT, int MT>
+int waves_for(int K) {
+  return (K > 2048 && MT <= 32) ? 12 : 8;
+}
+
+template <class DT, int MT>
+const void* kernel_for(int waves) {
+  if constexpr (MT <= 32) {
+    if (waves == 12) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 12>);
+  }
+  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8>);
 }
 
 template <class DT>
 hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
   void* args[] = {const_cast<Int4LinearParams*>(&p)};
   const void* fn;
-  int mt;
+  int mt, waves;
   if (p.M <= 16) {
-    fn = reinterpret_cast<const void*>(&int4_linear_kernel<DT, 16>);
     mt = 16;
+    waves = waves_for<DT, 16>(p.K);
+    fn = kernel_for<DT, 16>(waves);
   } else if (p.M <= 32) {
-    fn = reinterpret_cast<const void*>(&int4_linear_kernel<DT, 32>);
     mt = 32;
+    waves = waves_for<DT, 32>(p.K);
+    fn = kernel_for<DT, 32>(waves);
   } else {
-    fn = reinterpret_cast<const void*>(&int4_linear_kernel<DT, 64>);
     mt = 64;
+    waves = waves_for<DT, 64>(p.K);
+    fn = kernel_for<DT, 64>(waves);
   }
   const dim3 grid(static_cast<unsigned>(p.N / 16), static_cast<unsigned>((p.M + mt - 1) / mt));
-  return hipLaunchKernel(fn, grid, dim3(256), args, 0, stream);
+  return hipLaunchKernel(fn, grid, dim3(64 * waves), args, 0, stream);
 }
 
 bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; }
@@ -159,17 +261,21 @@ bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q)
 
 extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                               const void* qweight, const void* scales, const void* zeros, const void* bias,
+                              const void* residual, int epilogue,
                               int64_t M, int N, int K, int group_size, int dtype, void* stream) {
   using namespace ns;
   if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
   if (M < 0 || N <= 0 || K <= 0 || group_size <= 0) return NS_ERR_INVALID_ARG;
+  if (epilogue != NS_EPILOGUE_NONE && epilogue != NS_EPILOGUE_RESIDUAL && epilogue != NS_EPILOGUE_SILU_MUL)
+    return NS_ERR_UNSUPPORTED;
   if (M == 0) return NS_OK;
   if (!out || !x || !qweight || !scales || !zeros) return NS_ERR_INVALID_ARG;
+  if (epilogue == NS_EPILOGUE_RESIDUAL && (!residual || !aligned(residual, 8))) return NS_ERR_INVALID_ARG;
   // One MFMA row tile per 16 features; a K step of 32 lies inside one group.
   if (N % 16 != 0 || K % 32 != 0 || group_size % 32 != 0 || K % group_size != 0) return NS_ERR_UNSUPPORTED;
   if ((M + 15) / 16 > 65535) return NS_ERR_INVALID_ARG;  // grid.y bound of the smallest tile
   if (x_stride_row < K || x_stride_row % 8 != 0 || !aligned(x, 16) || !aligned(out, 8) ||
-      !aligned(qweight, 4) || !aligned(scales, 4) || (bias && !aligned(bias, 2)))
+      !aligned(qweight, 16) || !aligned(scales, 4) || (bias && !aligned(bias, 2)))
     return NS_ERR_INVALID_ARG;
 
   Int4LinearParams p;
@@ -180,6 +286,8 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   p.scales = static_cast<const float*>(scales);
   p.zeros = static_cast<const uint8_t*>(zeros);
   p.bias = bias;
+  p.residual = residual;
+  p.epilogue = epilogue;
   p.M = static_cast<int>(M);
   p.N = N;
   p.K = K;

@@ -31,6 +31,7 @@ import torch
 from .attention import AttentionMetadata, get_attention_backend
 from .block_manager import BlockSpaceManager
 from .kv_cache import PagedKVCache
+from .sampling import argmax_rows
 
 
 @dataclass
@@ -348,7 +349,7 @@ class ModelRunner:
         if sample_idx is None:
             return []
         logits = self.model.compute_logits(hidden, sample_idx)
-        tokens = logits.argmax(dim=-1).tolist()  # greedy; the step's one device-to-host sync
+        tokens = argmax_rows(logits).tolist()  # greedy; the step's one device-to-host sync
         return list(zip(sample_seqs, tokens))
 
 
@@ -424,7 +425,7 @@ class DecodeGraphs:
         def forward():
             hidden = r.model(ids, pos, r.kv_cache, md, r.attn_fn)
             logits = r.model.compute_logits(hidden)
-            return logits.argmax(dim=-1), logits
+            return argmax_rows(logits), logits
 
         s = self._stream
         s.wait_stream(torch.cuda.current_stream(r.device))

@@ -60,6 +60,14 @@ class RMSNorm(nn.Module):
         return F.rms_norm(x, (x.shape[-1],), self.weight, self.variance_epsilon)
 
 
+def _linear(mod: nn.Module, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
+    """mod(x) (+ residual): INT4 projections add the residual inside their launch."""
+    if isinstance(mod, Int4Linear):
+        return mod(x, residual=residual)
+    y = mod(x)
+    return y if residual is None else residual + y
+
+
 def _concat_linears(parts: list[nn.Module]) -> nn.Module:
     """One linear whose output rows are the parts' rows in order."""
     if all(isinstance(p, Int4Linear) for p in parts):
@@ -104,7 +112,8 @@ class Qwen2Attention(nn.Module):
         self.qkv_proj = _concat_linears([self.q_proj, self.k_proj, self.v_proj])
         del self.q_proj, self.k_proj, self.v_proj
 
-    def forward(self, hidden, cos, sin, kv_cache, md, attn_fn):
+    def forward(self, hidden, cos, sin, kv_cache, md, attn_fn, residual=None):
+        """Attention output projected by o_proj, plus `residual` when given."""
         T = hidden.shape[0]
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
         if self.qkv_proj is not None:
@@ -121,7 +130,7 @@ class Qwen2Attention(nn.Module):
         kc, vc = kv_cache.k_cache[self.layer_idx], kv_cache.v_cache[self.layer_idx]
         q = rope_reshape_and_cache(q, k, v, cos, sin, kc, vc, md.slot_mapping)
         out = attn_fn(q, kc, vc, md, self.scale)
-        return self.o_proj(out.view(T, Hq * D))
+        return _linear(self.o_proj, out.view(T, Hq * D), residual)
 
 
 class Qwen2MLP(nn.Module):
@@ -136,16 +145,26 @@ class Qwen2MLP(nn.Module):
         self.gate_up_proj: nn.Module | None = None
 
     def fuse(self) -> None:
-        self.gate_up_proj = _concat_linears([self.gate_proj, self.up_proj])
+        if isinstance(self.gate_proj, Int4Linear) and isinstance(self.up_proj, Int4Linear):
+            # One launch computes silu(gate) * up from interleaved rows.
+            self.gate_up_proj = Int4Linear.gate_up_pairs(self.gate_proj, self.up_proj)
+        else:
+            self.gate_up_proj = _concat_linears([self.gate_proj, self.up_proj])
         del self.gate_proj, self.up_proj
 
-    def forward(self, x):
-        if self.gate_up_proj is not None:
-            gu = self.gate_up_proj(x)
-            g, u = gu[:, :self.intermediate_size], gu[:, self.intermediate_size:]
+    def forward(self, x, residual=None):
+        """down(silu(gate(x)) * up(x)), plus `residual` when given."""
+        gu = self.gate_up_proj
+        if isinstance(gu, Int4Linear) and gu.silu_mul:
+            act = gu(x)
         else:
-            g, u = self.gate_proj(x), self.up_proj(x)
-        return self.down_proj(F.silu(g) * u)
+            if gu is not None:
+                y = gu(x)
+                g, u = y[:, :self.intermediate_size], y[:, self.intermediate_size:]
+            else:
+                g, u = self.gate_proj(x), self.up_proj(x)
+            act = F.silu(g) * u
+        return _linear(self.down_proj, act, residual)
 
 
 class Qwen2DecoderLayer(nn.Module):
@@ -157,8 +176,8 @@ class Qwen2DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
 
     def forward(self, hidden, cos, sin, kv_cache, md, attn_fn):
-        h = hidden + self.self_attn(self.input_layernorm(hidden), cos, sin, kv_cache, md, attn_fn)
-        return h + self.mlp(self.post_attention_layernorm(h))
+        h = self.self_attn(self.input_layernorm(hidden), cos, sin, kv_cache, md, attn_fn, residual=hidden)
+        return self.mlp(self.post_attention_layernorm(h), residual=h)
 
 
 class Qwen2Model(nn.Module):

@@ -47,8 +47,15 @@ def quantize_int4_groupwise(w: torch.Tensor, group_size: int = 128):
 
 @torch.inference_mode()
 def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
-                bias: torch.Tensor | None, group_size: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """x [..., K] -> [..., N] through ns_int4_linear (HIP; no CPU fallback)."""
+                bias: torch.Tensor | None, group_size: int, out: torch.Tensor | None = None,
+                residual: torch.Tensor | None = None, silu_mul: bool = False) -> torch.Tensor:
+    """x [..., K] -> [..., N] through ns_int4_linear (HIP; no CPU fallback).
+
+    residual: [..., N] added to the result in the same launch (the reference's
+    `residual + o_proj(x)`, rounded as two tensor ops).  silu_mul: the weight's
+    rows are interleaved (gate, up) pairs and the result is
+    silu(gate) * up, [..., N/2] (the reference SwiGLU, rounded per op).
+    """
     lib = _lib.load()
     N, half_k = qweight.shape
     K = 2 * half_k
@@ -64,22 +71,33 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
         raise ValueError("quantised weight tensors must be contiguous")
     if bias is not None and (bias.dtype != x.dtype or bias.shape != (N,) or not bias.is_contiguous()):
         raise ValueError(f"bias must be a contiguous [{N}] {x.dtype} tensor")
+    if silu_mul and residual is not None:
+        raise ValueError("silu_mul and residual are separate epilogues")
     lead = x.shape[:-1]
     x2 = x.reshape(-1, K)
     if x2.stride(1) != 1 or x2.stride(0) % 8 != 0 or x2.data_ptr() % 16 != 0:
         x2 = x2.contiguous()
     M = x2.shape[0]
+    n_out = N // 2 if silu_mul else N
+    epilogue = _lib.NS_EPILOGUE_SILU_MUL if silu_mul else _lib.NS_EPILOGUE_NONE
+    res_ptr = None
+    if residual is not None:
+        res = residual.reshape(-1, N)
+        if res.shape[0] != M or res.dtype != x.dtype or not res.is_contiguous():
+            raise ValueError(f"residual must be a contiguous [{M}, {N}] {x.dtype} tensor")
+        res_ptr = res.data_ptr()
+        epilogue = _lib.NS_EPILOGUE_RESIDUAL
     if out is None:
-        out = torch.empty((M, N), dtype=x.dtype, device=x.device)
-    elif out.shape != (M, N) or out.dtype != x.dtype or not out.is_contiguous():
-        raise ValueError(f"out must be a contiguous [{M}, {N}] {x.dtype} tensor")
+        out = torch.empty((M, n_out), dtype=x.dtype, device=x.device)
+    elif out.shape != (M, n_out) or out.dtype != x.dtype or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous [{M}, {n_out}] {x.dtype} tensor")
     rc = lib.ns_int4_linear(out.data_ptr(), x2.data_ptr(), x2.stride(0),
                             qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
-                            bias.data_ptr() if bias is not None else None,
+                            bias.data_ptr() if bias is not None else None, res_ptr, epilogue,
                             M, N, K, group_size, _lib.DTYPE_CODES[x.dtype],
                             torch.cuda.current_stream(x.device).cuda_stream)
     _lib.check(rc, "ns_int4_linear")
-    return out.view(*lead, N)
+    return out.view(*lead, n_out)
 
 
 class Int4Linear(nn.Module):
@@ -103,6 +121,8 @@ class Int4Linear(nn.Module):
         self.register_buffer("scales", torch.zeros(out_features, g, dtype=torch.float32, device=device))
         self.register_buffer("zeros", torch.zeros(out_features, g, dtype=torch.uint8, device=device))
         self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype, device=device)) if bias else None
+        # Rows interleaved as (gate, up) pairs whose output is silu(gate) * up.
+        self.silu_mul = False
 
     @classmethod
     def from_linear(cls, lin: nn.Linear, group_size: int = 128) -> "Int4Linear":
@@ -116,12 +136,27 @@ class Int4Linear(nn.Module):
             m.bias.data.copy_(lin.bias.data)
         return m
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def forward(self, x: torch.Tensor, residual: torch.Tensor | None = None) -> torch.Tensor:
         return int4_linear(x, self.qweight, self.scales, self.zeros,
-                           None if self.bias is None else self.bias.data, self.group_size)
+                           None if self.bias is None else self.bias.data, self.group_size,
+                           residual=residual, silu_mul=self.silu_mul)
+
+    @classmethod
+    def gate_up_pairs(cls, gate: "Int4Linear", up: "Int4Linear") -> "Int4Linear":
+        """One module computing silu(gate(x)) * up(x): rows interleaved gate_0, up_0, gate_1, ..."""
+        if gate.bias is not None or up.bias is not None or gate.qweight.shape != up.qweight.shape:
+            raise ValueError("gate/up must be bias-free projections of one shape")
+        m = cls(gate.in_features, 2 * gate.out_features, False, gate.group_size, gate.compute_dtype,
+                gate.qweight.device)
+        for name in ("qweight", "scales", "zeros"):
+            a, b = getattr(gate, name), getattr(up, name)
+            getattr(m, name).copy_(torch.stack([a, b], dim=1).reshape(-1, a.shape[1]))
+        m.silu_mul = True
+        return m
 
     def extra_repr(self) -> str:
-        return f"in={self.in_features}, out={self.out_features}, int4 group={self.group_size}"
+        extra = ", silu(gate)*up pairs" if self.silu_mul else ""
+        return f"in={self.in_features}, out={self.out_features}, int4 group={self.group_size}{extra}"
 
 
 def quantize_model(model: nn.Module, group_size: int = 128, skip: tuple[str, ...] = ("lm_head",)) -> dict:

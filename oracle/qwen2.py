@@ -81,7 +81,10 @@ def qwen2_forward_ref(model, input_ids, positions, k_caches, v_caches, md, sampl
         if mlp.gate_up_proj is not None:
             w, _ = _weight(mlp.gate_up_proj, name)
             gu = x @ w.T
-            g, u = gu[:, :cfg.intermediate_size], gu[:, cfg.intermediate_size:]
+            if getattr(mlp.gate_up_proj, "silu_mul", False):  # rows interleaved (gate_j, up_j)
+                g, u = gu[:, 0::2], gu[:, 1::2]
+            else:
+                g, u = gu[:, :cfg.intermediate_size], gu[:, cfg.intermediate_size:]
         else:
             g, u = x @ _weight(mlp.gate_proj, name)[0].T, x @ _weight(mlp.up_proj, name)[0].T
         wd, _ = _weight(mlp.down_proj, name)

@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for n in ("ns_reshape_and_cache", "ns_paged_attention", "ns_paged_attention_workspace_size",
-              "ns_rope_reshape_and_cache", "ns_int4_linear",
+              "ns_rope_reshape_and_cache", "ns_int4_linear", "ns_argmax_rows",
               "ns_error_string", "ns_version"):
         assert n in names
 
@@ -148,8 +148,8 @@ def test_rope_reshape_and_cache_zero_tokens_is_a_no_op():
 
 
 def _i4_args(**over):
-    a = dict(out=16, x=16, xs=256, qw=16, sc=16, zp=16, bias=None, M=4, N=64, K=256, gs=128,
-             dt=_lib.NS_DTYPE_F16, stream=None)
+    a = dict(out=16, x=16, xs=256, qw=16, sc=16, zp=16, bias=None, res=None, epi=_lib.NS_EPILOGUE_NONE,
+             M=4, N=64, K=256, gs=128, dt=_lib.NS_DTYPE_F16, stream=None)
     a.update(over)
     return list(a.values())
 
@@ -166,6 +166,9 @@ def _i4_args(**over):
     (dict(xs=128), _lib.NS_ERR_INVALID_ARG),              # row stride shorter than a row
     (dict(x=24), _lib.NS_ERR_INVALID_ARG),
     (dict(out=20), _lib.NS_ERR_INVALID_ARG),
+    (dict(qw=24), _lib.NS_ERR_INVALID_ARG),               # codes are read as 16-byte vectors
+    (dict(epi=3), _lib.NS_ERR_UNSUPPORTED),
+    (dict(epi=_lib.NS_EPILOGUE_RESIDUAL), _lib.NS_ERR_INVALID_ARG),  # residual epilogue without residual
 ])
 def test_int4_linear_rejects_bad_arguments(over, code):
     lib = _lib.load()
@@ -175,3 +178,15 @@ def test_int4_linear_rejects_bad_arguments(over, code):
 def test_int4_linear_zero_rows_is_a_no_op():
     lib = _lib.load()
     assert lib.ns_int4_linear(*_i4_args(M=0, x=None)) == _lib.NS_OK
+
+
+@pytest.mark.parametrize("args,code", [
+    ((16, 16, 100, 4, 100, 7, None), _lib.NS_ERR_UNSUPPORTED),
+    ((None, 16, 100, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),
+    ((16, 16, 99, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),   # stride shorter than a row
+    ((16, 16, 100, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),  # 200-byte rows, not 16-aligned
+    ((16, 24, 104, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),  # misaligned base
+    ((16, 16, 104, 0, 100, _lib.NS_DTYPE_F16, None), _lib.NS_OK),               # no rows: no launch
+])
+def test_argmax_rows_rejects_bad_arguments(args, code):
+    assert _lib.load().ns_argmax_rows(*args) == code
