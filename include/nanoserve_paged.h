@@ -152,10 +152,16 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
  * ([M, N] with row stride x_stride_row elements), the first such index on
  * ties and the first NaN if the row holds one: torch.argmax(dim=-1), which
  * the reference's greedy sampler calls (nanoserve/sampler.py:24-27).  out is
- * int64.  dtype is NS_DTYPE_F32, NS_DTYPE_F16 or NS_DTYPE_BF16.
+ * int64 [M]; x 16-byte aligned with 16-byte-multiple rows; M <= 65535 and
+ * N < 2^32.  dtype is NS_DTYPE_F32, NS_DTYPE_F16 or NS_DTYPE_BF16.  Each row
+ * is scanned in slices by separate workgroups whose results meet in
+ * `workspace` (ns_argmax_rows_workspace_size bytes, 8-byte aligned, no
+ * initialisation needed); calls that overlap in time need separate
+ * workspaces.  Returns NS_ERR_WORKSPACE when it is missing or too small.
  */
+size_t ns_argmax_rows_workspace_size(int64_t M, int64_t N);
 int ns_argmax_rows(int64_t* out, const void* x, int64_t x_stride_row, int64_t M, int64_t N,
-                   int dtype, void* stream);
+                   int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * ns_paged_attention_workspace_size -- bytes of device workspace that

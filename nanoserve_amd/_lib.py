@@ -69,9 +69,11 @@ SIGNATURES = {
         c_int64, c_int, c_int, c_int,            # M, N, K, group_size
         c_int, c_void_p,                         # dtype, stream
     ]),
+    "ns_argmax_rows_workspace_size": (c_size_t, [c_int64, c_int64]),  # M, N
     "ns_argmax_rows": (c_int, [
         c_void_p, c_void_p, c_int64,             # out (int64), x, x row stride
-        c_int64, c_int64, c_int, c_void_p,       # M, N, dtype, stream
+        c_int64, c_int64, c_int,                 # M, N, dtype
+        c_void_p, c_size_t, c_void_p,            # workspace, bytes, stream
     ]),
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,

@@ -67,11 +67,12 @@ __device__ __forceinline__ typename DT::vec8 dequant8(uint32_t word, float zero,
 // SiLU in float32 as torch evaluates it for half tensors: x / (1 + exp(-x)).
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-template <class DT, int MT, int WAVES>
+template <class DT, int MT, int WAVES, int BATCH>
 __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParams p) {
+  // BATCH: 128-wide chunks whose weights one wave loads at once (1 when every
+  // wave has a single chunk, which keeps the register count low).
   constexpr int NT = MT / 16;  // MFMA column tiles
   constexpr int ESZ = sizeof(typename DT::T);
-  constexpr int BATCH = 4;     // 128-wide chunks whose weights one wave loads at once
   using V8 = typename DT::vec8;
   using T = typename DT::T;
   const int lane = threadIdx.x & 63;
@@ -174,17 +175,19 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   }
 
   // Waves 1.. hand their partial sums to wave 0.
-  __shared__ floatx4 red[WAVES - 1][NT][64];
-  if (wave > 0) {
+  if constexpr (WAVES > 1) {
+    __shared__ floatx4 red[WAVES - 1][NT][64];
+    if (wave > 0) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
-  }
-  __syncthreads();
-  if (wave != 0) return;
+      for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
+    }
+    __syncthreads();
+    if (wave != 0) return;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
+    for (int t = 0; t < NT; ++t) {
 #pragma unroll
-    for (int w = 0; w < WAVES - 1; ++w) acc[t] += red[w][t][lane];
+      for (int w = 0; w < WAVES - 1; ++w) acc[t] += red[w][t][lane];
+    }
   }
 
   // D[4·(lane/16) + r][lane%16]: features nf .. nf+3 of token m.  Each
@@ -216,42 +219,55 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   }
 }
 
-// Waves per workgroup: enough that each keeps a few 128-wide chunks in flight
-// for long K (down_proj's 4864 is 38 chunks), within the VGPR budget of the
-// tile: 12 waves (3 per SIMD) for up to 32 tokens, 8 otherwise.
-template <class DT, int MT>
-int waves_for(int K) {
-  return (K > 2048 && MT <= 32) ? 12 : 8;
+// Launch shape.  K of up to 2048 (Qwen2.5-0.5B: 896) gets one wave per
+// 128-wide chunk, up to 8 waves, each with a single chunk (few registers, so
+// many waves fit per SIMD).  Longer K (down_proj's 4864 = 38 chunks) gets 16
+// waves per 16-token tile (8 per 64-token tile) that each fetch up to four
+// chunks at once.
+struct Shape {
+  int waves;
+  int batch;
+};
+
+Shape shape_for(int K, int mt) {
+  const int chunks = K / 128;
+  if (chunks >= 1 && chunks <= 8) return {chunks, 1};
+  if (K <= 2048) return {8, 4};
+  return {mt <= 16 ? 16 : 8, 4};
 }
 
 template <class DT, int MT>
-const void* kernel_for(int waves) {
-  if constexpr (MT <= 32) {
-    if (waves == 12) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 12>);
+const void* kernel_for(Shape sh) {
+  if (sh.batch == 1) {
+    switch (sh.waves) {
+      case 1: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 1, 1>);
+      case 2: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 2, 1>);
+      case 3: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 3, 1>);
+      case 4: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 4, 1>);
+      case 5: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 5, 1>);
+      case 6: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 6, 1>);
+      case 7: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 7, 1>);
+      default: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 1>);
+    }
   }
-  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8>);
+  if constexpr (MT <= 16) {
+    if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4>);
+  }
+  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 4>);
 }
 
 template <class DT>
 hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
   void* args[] = {const_cast<Int4LinearParams*>(&p)};
-  const void* fn;
-  int mt, waves;
-  if (p.M <= 16) {
-    mt = 16;
-    waves = waves_for<DT, 16>(p.K);
-    fn = kernel_for<DT, 16>(waves);
-  } else if (p.M <= 32) {
-    mt = 32;
-    waves = waves_for<DT, 32>(p.K);
-    fn = kernel_for<DT, 32>(waves);
-  } else {
-    mt = 64;
-    waves = waves_for<DT, 64>(p.K);
-    fn = kernel_for<DT, 64>(waves);
-  }
+  // Up to 64 tokens, 16-token tiles (grid.y tiles side by side) beat wider
+  // ones: more waves in flight and fewer registers each (measured on MI355X,
+  // M = 32: down_proj 12.9 -> 8.5 us, qkv 4.1 -> 3.3 us).  Beyond that, 64-token
+  // tiles amortise the dequantisation over more MFMAs.
+  const int mt = p.M <= 64 ? 16 : 64;
+  const Shape sh = shape_for(p.K, mt);
+  const void* fn = mt == 16 ? kernel_for<DT, 16>(sh) : kernel_for<DT, 64>(sh);
   const dim3 grid(static_cast<unsigned>(p.N / 16), static_cast<unsigned>((p.M + mt - 1) / mt));
-  return hipLaunchKernel(fn, grid, dim3(64 * waves), args, 0, stream);
+  return hipLaunchKernel(fn, grid, dim3(64 * sh.waves), args, 0, stream);
 }
 
 bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; }

@@ -11,6 +11,19 @@ import torch
 
 from . import _lib
 
+# One slice-key workspace per (device, stream), grown on demand; graph capture
+# records its pointer, so it is allocated by the warm-up call before capture.
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
 
 @torch.inference_mode()
 def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -31,7 +44,10 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.
     M, N = logits.shape
     if out is None:
         out = torch.empty(M, dtype=torch.int64, device=x.device)
-    rc = _lib.load().ns_argmax_rows(out.data_ptr(), x.data_ptr(), x.stride(0), M, N,
-                                    _lib.DTYPE_CODES[x.dtype], torch.cuda.current_stream(x.device).cuda_stream)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    ws = _workspace(x.device, stream, lib.ns_argmax_rows_workspace_size(M, N))
+    rc = lib.ns_argmax_rows(out.data_ptr(), x.data_ptr(), x.stride(0), M, N, _lib.DTYPE_CODES[x.dtype],
+                            ws.data_ptr(), ws.numel(), stream)
     _lib.check(rc, "ns_argmax_rows")
     return out

@@ -55,6 +55,15 @@ def test_ties_pick_the_first_index_and_nan_wins(dtype):
     assert got.tolist() == torch.argmax(x.to(DEV), dim=-1).tolist()
 
 
+def test_signed_zeros_are_equal():
+    x = torch.full((2, 9000), -1.0)
+    x[0, 3], x[0, 7] = -0.0, 0.0          # equal maxima: the first wins
+    x[1, 8191], x[1, 8192] = 0.0, -0.0    # across a slice boundary
+    got = argmax_rows(x.half().to(DEV))
+    torch.cuda.synchronize()
+    assert got.tolist() == [3, 8191]
+
+
 def test_strided_rows_and_unaligned_width():
     g = torch.Generator().manual_seed(3)
     wide = torch.randn(6, 1030, generator=g).half().to(DEV)

@@ -181,12 +181,21 @@ def test_int4_linear_zero_rows_is_a_no_op():
 
 
 @pytest.mark.parametrize("args,code", [
-    ((16, 16, 100, 4, 100, 7, None), _lib.NS_ERR_UNSUPPORTED),
-    ((None, 16, 100, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),
-    ((16, 16, 99, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),   # stride shorter than a row
-    ((16, 16, 100, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),  # 200-byte rows, not 16-aligned
-    ((16, 24, 104, 4, 100, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),  # misaligned base
-    ((16, 16, 104, 0, 100, _lib.NS_DTYPE_F16, None), _lib.NS_OK),               # no rows: no launch
+    ((16, 16, 104, 4, 100, 7, 16, 1 << 20, None), _lib.NS_ERR_UNSUPPORTED),
+    ((None, 16, 104, 4, 100, _lib.NS_DTYPE_F16, 16, 1 << 20, None), _lib.NS_ERR_INVALID_ARG),
+    ((16, 16, 99, 4, 100, _lib.NS_DTYPE_F16, 16, 1 << 20, None), _lib.NS_ERR_INVALID_ARG),   # stride < row
+    ((16, 16, 100, 4, 100, _lib.NS_DTYPE_F16, 16, 1 << 20, None), _lib.NS_ERR_INVALID_ARG),  # 200-byte rows
+    ((16, 24, 104, 4, 100, _lib.NS_DTYPE_F16, 16, 1 << 20, None), _lib.NS_ERR_INVALID_ARG),  # misaligned base
+    ((16, 16, 104, 4, 100, _lib.NS_DTYPE_F16, None, 0, None), _lib.NS_ERR_WORKSPACE),
+    ((16, 16, 104, 4, 100, _lib.NS_DTYPE_F16, 16, 8, None), _lib.NS_ERR_WORKSPACE),          # 4 rows need 32 B
+    ((16, 16, 104, 0, 100, _lib.NS_DTYPE_F16, None, 0, None), _lib.NS_OK),                   # no rows: no launch
 ])
 def test_argmax_rows_rejects_bad_arguments(args, code):
     assert _lib.load().ns_argmax_rows(*args) == code
+
+
+def test_argmax_workspace_size():
+    lib = _lib.load()
+    assert lib.ns_argmax_rows_workspace_size(32, 151936) == 32 * 38 * 8
+    assert lib.ns_argmax_rows_workspace_size(1, 4096) == 8
+    assert lib.ns_argmax_rows_workspace_size(0, 10) == 0
