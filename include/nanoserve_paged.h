@@ -138,14 +138,30 @@ int ns_rope_reshape_and_cache(void* q_out, const void* query,
  *   NS_EPILOGUE_SILU_MUL  W's rows are interleaved (gate_j, up_j) pairs and
  *                         out [M, N/2] = round(round(silu(gate)) * up): the
  *                         SwiGLU of reference layers.py:108-109.
+ * With norm_weight (a [K] `dtype` vector, 16-byte aligned) the rows of x are
+ * first RMS-normalised in the same launch, round((x * rsqrt(mean(x^2) + eps))
+ * * norm_weight), as torch's F.rms_norm computes the reference's RMSNorm
+ * (layers.py:25-47) before q/k/v and gate/up; this needs K a multiple of 128
+ * and at most 1024.
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16.  N must be a multiple of 16, K and
  * group_size multiples of 32 with K a multiple of group_size; qweight 16-byte
  * aligned, out 8-byte aligned.
  */
 int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                    const void* qweight, const void* scales, const void* zeros, const void* bias,
-                   const void* residual, int epilogue,
+                   const void* residual, int epilogue, const void* norm_weight, float norm_eps,
                    int64_t M, int N, int K, int group_size, int dtype, void* stream);
+
+/*
+ * ns_int4_dequantize -- out [N, K] (`dtype`, contiguous, 16-byte aligned) =
+ * the model-dtype weights of an INT4 layer: dequantize_int4 (reference
+ * nanoserve/quant.py:83-95), bit for bit, in one pass.  For large token
+ * counts a library GEMM on this weight is faster than ns_int4_linear, which
+ * dequantises each weight tile once per 64-token tile.  K and group_size
+ * multiples of 8, K a multiple of group_size.
+ */
+int ns_int4_dequantize(void* out, const void* qweight, const void* scales, const void* zeros,
+                       int N, int K, int group_size, int dtype, void* stream);
 
 /*
  * ns_argmax_rows -- out[m] = index of the largest element of row m of x

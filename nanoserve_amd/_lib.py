@@ -66,8 +66,13 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int64,             # out, x, x row stride
         c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)
         c_void_p, c_int,                         # residual (or None), epilogue
+        c_void_p, c_float,                       # RMSNorm weight (or None), eps
         c_int64, c_int, c_int, c_int,            # M, N, K, group_size
         c_int, c_void_p,                         # dtype, stream
+    ]),
+    "ns_int4_dequantize": (c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p,  # out [N, K], qweight, scales, zeros
+        c_int, c_int, c_int, c_int, c_void_p,    # N, K, group_size, dtype, stream
     ]),
     "ns_argmax_rows_workspace_size": (c_size_t, [c_int64, c_int64]),  # M, N
     "ns_argmax_rows": (c_int, [

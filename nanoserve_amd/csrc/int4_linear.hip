@@ -38,6 +38,8 @@ struct Int4LinearParams {
   const uint8_t* zeros;   // [N, G]
   const void* bias;       // [N] model dtype, or null
   const void* residual;   // [M, N] contiguous, model dtype (NS_EPILOGUE_RESIDUAL)
+  const void* norm_weight; // [K] model dtype: RMSNorm the rows of x first (or null)
+  float norm_eps;
   int epilogue;
   int M, N, K, group_size, groups;
 };
@@ -123,9 +125,67 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 #pragma unroll
   for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+  if constexpr (BATCH == 1) {
+    if (p.norm_weight) {
+      // RMSNorm prologue (the host guarantees one 128-wide chunk per wave):
+      // every wave already holds its slice of each x row, so the rows' sums
+      // of squares meet in LDS and the operands are scaled in registers,
+      // y = round((x * rsqrt(mean(x^2) + eps)) * w) as torch's fused
+      // rms_norm evaluates it.
+      const int kb = 128 * wave + 32 * grp;
+      const u32x4 codes = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
+      const int gi = kb / p.group_size;
+      const float scale = srow[gi];
+      const float zero = static_cast<float>(zrow[gi]);
+      V8 b[4][NT], nw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        nw[j] = load16<DT>(static_cast<const char*>(p.norm_weight) + (kb + 8 * j) * ESZ);
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+          b[j][t] = xok[t] ? load16<DT>(xrow[t] + (kb + 8 * j) * ESZ) : zero8<DT>();
+      }
+      __shared__ float nss[WAVES][NT][16];
+      float ss[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        ss[t] = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float v = static_cast<float>(b[j][t][e]);
+            ss[t] += v * v;
+          }
+        ss[t] += __shfl_xor(ss[t], 16);  // the four lane groups holding this row
+        ss[t] += __shfl_xor(ss[t], 32);
+        if (grp == 0) nss[wave][t][row] = ss[t];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) tot += nss[w][t][row];
+        const float rstd = rsqrtf(tot / static_cast<float>(p.K) + p.norm_eps);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            b[j][t][e] = to_model<DT>(static_cast<float>(b[j][t][e]) * rstd * static_cast<float>(nw[j][e]));
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const V8 a = dequant8<DT>(codes[j], zero, scale);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+      }
+    }
+  }
+
   // Whole 128-wide chunks, split between the waves; each wave fetches the
   // codes, scales and zeros of up to BATCH chunks before using any of them.
-  const int chunks = p.K / 128;
+  const int chunks = p.norm_weight ? 0 : p.K / 128;
   const int c_end = (chunks * (wave + 1)) / WAVES;
   for (int c0 = (chunks * wave) / WAVES; c0 < c_end; c0 += BATCH) {
     const int nb = c_end - c0 < BATCH ? c_end - c0 : BATCH;
@@ -162,7 +222,7 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
   }
   // Remaining 32-wide steps when K is not a multiple of 128.
-  for (int s = 4 * chunks + wave; s < p.K / 32; s += WAVES) {
+  for (int s = p.norm_weight ? p.K / 32 : 4 * chunks + wave; s < p.K / 32; s += WAVES) {
     const int k = 32 * s + 8 * grp;
     const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow + k / 2);
     const int gi = k / p.group_size;
@@ -272,12 +332,30 @@ hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
 
 bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; }
 
+// Whole-weight dequantisation for large token counts, where a library GEMM on
+// the model-dtype weight beats re-dequantising each weight tile per token
+// tile.  One thread turns one 32-bit word (8 codes) into 16 bytes of weights,
+// with dequantize_int4's arithmetic (quant.py:83-95).
+template <class DT>
+__global__ __launch_bounds__(256) void int4_dequantize_kernel(typename DT::T* out, const uint8_t* qweight,
+                                                              const float* scales, const uint8_t* zeros,
+                                                              int64_t words, int K, int group_size, int groups) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= words) return;
+  const int64_t n = i / (K / 8);
+  const int k = static_cast<int>(i % (K / 8)) * 8;
+  const uint32_t word = reinterpret_cast<const uint32_t*>(qweight)[i];
+  const int gi = k / group_size;
+  const typename DT::vec8 w = dequant8<DT>(word, static_cast<float>(zeros[n * groups + gi]), scales[n * groups + gi]);
+  *reinterpret_cast<typename DT::vec8*>(out + n * K + k) = w;
+}
+
 }  // namespace
 }  // namespace ns
 
 extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                               const void* qweight, const void* scales, const void* zeros, const void* bias,
-                              const void* residual, int epilogue,
+                              const void* residual, int epilogue, const void* norm_weight, float norm_eps,
                               int64_t M, int N, int K, int group_size, int dtype, void* stream) {
   using namespace ns;
   if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
@@ -287,6 +365,9 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   if (M == 0) return NS_OK;
   if (!out || !x || !qweight || !scales || !zeros) return NS_ERR_INVALID_ARG;
   if (epilogue == NS_EPILOGUE_RESIDUAL && (!residual || !aligned(residual, 8))) return NS_ERR_INVALID_ARG;
+  // The RMSNorm prologue needs every 128-wide chunk of K on its own wave.
+  if (norm_weight && (K % 128 != 0 || K / 128 > 8)) return NS_ERR_UNSUPPORTED;
+  if (norm_weight && !aligned(norm_weight, 16)) return NS_ERR_INVALID_ARG;
   // One MFMA row tile per 16 features; a K step of 32 lies inside one group.
   if (N % 16 != 0 || K % 32 != 0 || group_size % 32 != 0 || K % group_size != 0) return NS_ERR_UNSUPPORTED;
   if ((M + 15) / 16 > 65535) return NS_ERR_INVALID_ARG;  // grid.y bound of the smallest tile
@@ -303,6 +384,8 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   p.zeros = static_cast<const uint8_t*>(zeros);
   p.bias = bias;
   p.residual = residual;
+  p.norm_weight = norm_weight;
+  p.norm_eps = norm_eps;
   p.epilogue = epilogue;
   p.M = static_cast<int>(M);
   p.N = N;
@@ -311,5 +394,28 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   p.groups = K / group_size;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s) : launch_int4_linear<BF16>(p, s);
+  return e == hipSuccess ? NS_OK : NS_ERR_HIP;
+}
+
+extern "C" int ns_int4_dequantize(void* out, const void* qweight, const void* scales, const void* zeros,
+                                  int N, int K, int group_size, int dtype, void* stream) {
+  using namespace ns;
+  if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
+  if (N <= 0 || K <= 0 || group_size <= 0) return NS_ERR_INVALID_ARG;
+  if (!out || !qweight || !scales || !zeros) return NS_ERR_INVALID_ARG;
+  if (K % 8 != 0 || group_size % 8 != 0 || K % group_size != 0) return NS_ERR_UNSUPPORTED;
+  if (!aligned(out, 16) || !aligned(qweight, 4) || !aligned(scales, 4)) return NS_ERR_INVALID_ARG;
+  const int64_t words = static_cast<int64_t>(N) * (K / 8);
+  const int64_t blocks = (words + 255) / 256;
+  if (blocks > 0x7FFFFFFF) return NS_ERR_INVALID_ARG;
+  const uint8_t* q = static_cast<const uint8_t*>(qweight);
+  const float* sc = static_cast<const float*>(scales);
+  const uint8_t* z = static_cast<const uint8_t*>(zeros);
+  int k = K, gs = group_size, g = K / group_size;
+  void* args[] = {&out, &q, &sc, &z, const_cast<int64_t*>(&words), &k, &gs, &g};
+  const void* fn = dtype == NS_DTYPE_F16 ? reinterpret_cast<const void*>(&int4_dequantize_kernel<F16>)
+                                         : reinterpret_cast<const void*>(&int4_dequantize_kernel<BF16>);
+  const hipError_t e = hipLaunchKernel(fn, dim3(static_cast<unsigned>(blocks)), dim3(256), args, 0,
+                                       static_cast<hipStream_t>(stream));
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }

@@ -112,12 +112,15 @@ class Qwen2Attention(nn.Module):
         self.qkv_proj = _concat_linears([self.q_proj, self.k_proj, self.v_proj])
         del self.q_proj, self.k_proj, self.v_proj
 
-    def forward(self, hidden, cos, sin, kv_cache, md, attn_fn, residual=None):
-        """Attention output projected by o_proj, plus `residual` when given."""
+    def forward(self, hidden, cos, sin, kv_cache, md, attn_fn, residual=None, norm=None):
+        """o_proj(attention(norm(hidden))) (+ residual).  `norm` (the layer's
+        input RMSNorm) runs inside the fused INT4 q|k|v launch when it can."""
         T = hidden.shape[0]
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
+        if norm is not None and not (isinstance(self.qkv_proj, Int4Linear) and self.qkv_proj.fuses_norm):
+            hidden, norm = norm(hidden), None
         if self.qkv_proj is not None:
-            qkv = self.qkv_proj(hidden)
+            qkv = self.qkv_proj(hidden, norm=norm) if norm is not None else self.qkv_proj(hidden)
             q = qkv[:, :Hq * D].view(T, Hq, D)
             k = qkv[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D)
             v = qkv[:, (Hq + Hkv) * D:].view(T, Hkv, D)
@@ -152,12 +155,15 @@ class Qwen2MLP(nn.Module):
             self.gate_up_proj = _concat_linears([self.gate_proj, self.up_proj])
         del self.gate_proj, self.up_proj
 
-    def forward(self, x, residual=None):
-        """down(silu(gate(x)) * up(x)), plus `residual` when given."""
+    def forward(self, x, residual=None, norm=None):
+        """down(silu(gate(norm(x))) * up(norm(x))) (+ residual); the RMSNorm runs
+        inside the fused INT4 gate|up launch when it can."""
         gu = self.gate_up_proj
         if isinstance(gu, Int4Linear) and gu.silu_mul:
-            act = gu(x)
+            act = gu(x, norm=norm)  # normalises first when the layer does not fuse it
         else:
+            if norm is not None:
+                x = norm(x)
             if gu is not None:
                 y = gu(x)
                 g, u = y[:, :self.intermediate_size], y[:, self.intermediate_size:]
@@ -176,8 +182,8 @@ class Qwen2DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
 
     def forward(self, hidden, cos, sin, kv_cache, md, attn_fn):
-        h = self.self_attn(self.input_layernorm(hidden), cos, sin, kv_cache, md, attn_fn, residual=hidden)
-        return self.mlp(self.post_attention_layernorm(h), residual=h)
+        h = self.self_attn(hidden, cos, sin, kv_cache, md, attn_fn, residual=hidden, norm=self.input_layernorm)
+        return self.mlp(h, residual=h, norm=self.post_attention_layernorm)
 
 
 class Qwen2Model(nn.Module):

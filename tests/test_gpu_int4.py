@@ -195,3 +195,71 @@ def test_silu_mul_epilogue_on_interleaved_gate_up(dtype, M):
     sep = torch.nn.functional.silu(qg(x.to(DEV))) * qu(x.to(DEV))
     torch.cuda.synchronize()
     assert (np.abs(sep.double().cpu().numpy() - want) <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K,M", [(896, 1), (896, 32), (896, 100), (256, 7), (1024, 40)])
+def test_rmsnorm_prologue(dtype, K, M):
+    """int4_linear(x, norm_weight=w) == linear(round((x * rsqrt(mean(x^2) + eps)) * w))."""
+    N = 1152
+    packed, s, z = _weights(N, K, 128, 21)
+    g = torch.Generator().manual_seed(22)
+    x = (torch.randn(M, K, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype)
+    got = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), b.to(DEV), 128,
+                      norm_weight=w.to(DEV), norm_eps=1e-6)
+    torch.cuda.synchronize()
+    xf = x.double().numpy()
+    rstd = 1.0 / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    xn = _round(xf * rstd * w.double().numpy(), dtype)
+    wq = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), 128, NAME[dtype])
+    ref = int4_linear_ref(xn, wq, b.float().numpy())
+    # The normalised operands may round one unit apart (rsqrt and sum order),
+    # which moves the result by at most that unit times |w| summed over K.
+    tol = 2 * RTOL[dtype] * np.abs(xn) @ np.abs(wq).T + RTOL[dtype] * np.abs(ref) + 1e-4
+    err = np.abs(got.double().cpu().numpy() - ref)
+    assert (err <= tol).all(), f"max err {err.max():.3e}"
+    # Same result as normalising with torch first.
+    sep = int4_linear(torch.nn.functional.rms_norm(x.to(DEV), (K,), w.to(DEV), 1e-6), packed.to(DEV),
+                      s.to(DEV), z.to(DEV), b.to(DEV), 128)
+    torch.cuda.synchronize()
+    assert (np.abs(sep.double().cpu().numpy() - ref) <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,K,gs", [(1152, 896, 128), (896, 4864, 128), (64, 256, 32)])
+def test_dequantize_is_bit_exact(dtype, N, K, gs):
+    from nanoserve_amd.quant import int4_dequantize
+
+    packed, s, z = _weights(N, K, gs, 31, scale=0.7)
+    got = int4_dequantize(packed.to(DEV), s.to(DEV), z.to(DEV), gs, dtype)
+    torch.cuda.synchronize()
+    want = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), gs, NAME[dtype])
+    assert np.array_equal(got.float().cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("M", [129, 700, 2048])
+def test_large_row_counts_take_the_dequant_path_within_one_rounding(M):
+    _run(M, 1152, 896, torch.float16, seed=M)
+    _run(M, 896, 4864, torch.bfloat16, seed=M + 1)
+
+
+@pytest.mark.parametrize("method", ["fused", "dequant"])
+def test_both_methods_agree_on_every_epilogue(method):
+    K, I = 896, 1024
+    g = torch.Generator().manual_seed(41)
+    pk, s, z = _weights(2 * I, K, 128, 42)
+    pk, s, z = pk.to(DEV), s.to(DEV), z.to(DEV)
+    x = torch.randn(200, K, generator=g).half().to(DEV)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).half().to(DEV)
+    res = torch.randn(200, 2 * I, generator=g).half().to(DEV)
+    outs = {}
+    for m in ("fused", "dequant"):
+        outs[m] = (int4_linear(x, pk, s, z, None, 128, method=m, silu_mul=True),
+                   int4_linear(x, pk, s, z, None, 128, method=m, residual=res),
+                   int4_linear(x, pk, s, z, None, 128, method=m, norm_weight=w))
+    torch.cuda.synchronize()
+    for a, b in zip(outs["fused"], outs["dequant"]):
+        err = (a.float() - b.float()).abs()
+        assert (err <= 4 * 2.0 ** -10 * b.float().abs() + 1e-3).all(), f"max err {err.max().item():.3e}"

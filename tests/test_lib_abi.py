@@ -24,7 +24,7 @@ def _declared_functions() -> list[str]:
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     for n in ("ns_reshape_and_cache", "ns_paged_attention", "ns_paged_attention_workspace_size",
-              "ns_rope_reshape_and_cache", "ns_int4_linear", "ns_argmax_rows",
+              "ns_rope_reshape_and_cache", "ns_int4_linear", "ns_int4_dequantize", "ns_argmax_rows",
               "ns_error_string", "ns_version"):
         assert n in names
 
@@ -149,7 +149,7 @@ def test_rope_reshape_and_cache_zero_tokens_is_a_no_op():
 
 def _i4_args(**over):
     a = dict(out=16, x=16, xs=256, qw=16, sc=16, zp=16, bias=None, res=None, epi=_lib.NS_EPILOGUE_NONE,
-             M=4, N=64, K=256, gs=128, dt=_lib.NS_DTYPE_F16, stream=None)
+             nw=None, eps=1e-6, M=4, N=64, K=256, gs=128, dt=_lib.NS_DTYPE_F16, stream=None)
     a.update(over)
     return list(a.values())
 
@@ -169,6 +169,9 @@ def _i4_args(**over):
     (dict(qw=24), _lib.NS_ERR_INVALID_ARG),               # codes are read as 16-byte vectors
     (dict(epi=3), _lib.NS_ERR_UNSUPPORTED),
     (dict(epi=_lib.NS_EPILOGUE_RESIDUAL), _lib.NS_ERR_INVALID_ARG),  # residual epilogue without residual
+    (dict(nw=16, K=2048, xs=2048), _lib.NS_ERR_UNSUPPORTED),          # RMSNorm prologue: K at most 1024
+    (dict(nw=16, K=96, xs=96, gs=32), _lib.NS_ERR_UNSUPPORTED),       # RMSNorm prologue: whole 128-chunks
+    (dict(nw=24), _lib.NS_ERR_INVALID_ARG),                          # misaligned norm weight
 ])
 def test_int4_linear_rejects_bad_arguments(over, code):
     lib = _lib.load()
@@ -199,3 +202,14 @@ def test_argmax_workspace_size():
     assert lib.ns_argmax_rows_workspace_size(32, 151936) == 32 * 38 * 8
     assert lib.ns_argmax_rows_workspace_size(1, 4096) == 8
     assert lib.ns_argmax_rows_workspace_size(0, 10) == 0
+
+
+@pytest.mark.parametrize("args,code", [
+    ((None, 16, 16, 16, 64, 256, 128, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),
+    ((16, 16, 16, 16, 64, 256, 128, _lib.NS_DTYPE_F32, None), _lib.NS_ERR_UNSUPPORTED),
+    ((16, 16, 16, 16, 64, 260, 130, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_UNSUPPORTED),
+    ((24, 16, 16, 16, 64, 256, 128, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),
+    ((16, 16, 16, 16, 0, 256, 128, _lib.NS_DTYPE_F16, None), _lib.NS_ERR_INVALID_ARG),
+])
+def test_int4_dequantize_rejects_bad_arguments(args, code):
+    assert _lib.load().ns_int4_dequantize(*args) == code
