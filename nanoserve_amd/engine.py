@@ -365,8 +365,12 @@ class DecodeGraphs:
     with slot -1 (the cache write skips it) and length 1.
 
     Attention inside the graph gets no host lengths, so it runs its full-grid
-    decode (splits sized for max_model_len, empty splits exit at once); the
-    block tables have max_model_len / block_size columns.
+    decode: splits sized for the graph's context bound, empty splits exiting
+    at once.  Graphs are therefore also keyed by a context bucket (powers of
+    two up to max_model_len): sizing the grid for 4096 tokens when the batch's
+    longest context is under 1024 doubles the attention time (MI355X, 32
+    sequences: 18.9 us against 9.5 us).  The block tables always have
+    max_model_len / block_size columns.
     """
 
     def __init__(self, runner: "ModelRunner", sizes: tuple[int, ...], max_model_len: int) -> None:
@@ -374,11 +378,13 @@ class DecodeGraphs:
         self.sizes = sorted(sizes)
         self.max_model_len = max_model_len
         self.width = -(-max_model_len // runner.block_size)
+        self.ctx_sizes = sorted({max_model_len >> k for k in range(4) if (max_model_len >> k) >= 256}
+                                | {max_model_len})
         n = max(self.sizes)
         self._per = 4 * n + n * self.width  # ids, pos, slots, lens, tables
         self._host = torch.empty(self._per, dtype=torch.int64, pin_memory=runner.device.type == "cuda")
         self._dev = torch.zeros(self._per, dtype=torch.int64, device=runner.device)
-        self._graphs: dict[int, tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        self._graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.last_logits: torch.Tensor | None = None  # graph-owned logits of the latest replay
         self._pool = None
         self._stream = torch.cuda.Stream(runner.device) if runner.device.type == "cuda" else None
@@ -393,11 +399,11 @@ class DecodeGraphs:
         return (d[0:b], d[n:n + b], d[2 * n:2 * n + b], d[3 * n:3 * n + b],
                 d[4 * n:4 * n + b * self.width].view(b, self.width))
 
-    def _metadata(self, b: int) -> tuple[torch.Tensor, torch.Tensor, AttentionMetadata]:
+    def _metadata(self, b: int, ctx: int) -> tuple[torch.Tensor, torch.Tensor, AttentionMetadata]:
         ids, pos, slots, lens, tables = self._views(b)
         md = AttentionMetadata(
             slot_mapping=slots, query_start_loc=None, seq_lens=lens, block_tables=tables,
-            max_query_len=1, max_seq_len=self.max_model_len, num_seqs=b, num_tokens=b,
+            max_query_len=1, max_seq_len=ctx, num_seqs=b, num_tokens=b,
             is_decode_only=True, query_lens_cpu=None, seq_lens_cpu=None, query_start_loc_cpu=None)
         return ids, pos, md
 
@@ -418,9 +424,9 @@ class DecodeGraphs:
         self._host.copy_(torch.from_numpy(h))
         self._dev.copy_(self._host)  # ordered before the replay on the same stream
 
-    def _capture(self, b: int):
+    def _capture(self, b: int, ctx: int):
         r = self.runner
-        ids, pos, md = self._metadata(b)
+        ids, pos, md = self._metadata(b, ctx)
 
         def forward():
             hidden = r.model(ids, pos, r.kv_cache, md, r.attn_fn)
@@ -438,23 +444,26 @@ class DecodeGraphs:
             out, logits = forward()
         if self._pool is None:
             self._pool = g.pool()
-        self._graphs[b] = (g, out, logits)
+        self._graphs[(b, ctx)] = (g, out, logits)
 
     def capture_all(self) -> None:
         """Capture every bucket up front, largest first (the pool then fits the rest)."""
         self._dev.zero_()
         self._dev[3 * max(self.sizes):4 * max(self.sizes)] = 1
         self._dev[2 * max(self.sizes):3 * max(self.sizes)] = -1
-        for b in sorted(self.sizes, reverse=True):
-            if b not in self._graphs:
-                self._capture(b)
+        for ctx in sorted(self.ctx_sizes, reverse=True):
+            for b in sorted(self.sizes, reverse=True):
+                if (b, ctx) not in self._graphs:
+                    self._capture(b, ctx)
 
     def execute(self, scheduled) -> list[tuple[Sequence, int]]:
         r = self.runner
         b = next(x for x in self.sizes if x >= len(scheduled))
-        if b not in self._graphs:
+        longest = max(seq.num_computed_tokens + 1 for seq, _ in scheduled)
+        ctx = next(c for c in self.ctx_sizes if c >= longest)
+        if (b, ctx) not in self._graphs:
             self.capture_all()
-        g, out, logits = self._graphs[b]
+        g, out, logits = self._graphs[(b, ctx)]
         self._fill(scheduled, b)
         g.replay()
         self.last_logits = logits[:len(scheduled)]

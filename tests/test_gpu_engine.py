@@ -232,3 +232,36 @@ def test_engine_with_graphs_completes_the_same_requests():
     same = sum(a == b for x, y in zip(eager, graphed) for a, b in zip(x, y))
     total = sum(len(x) for x in eager)
     assert same >= 0.9 * total, f"{same}/{total} tokens agree"
+
+
+def test_decode_graphs_switch_context_buckets_as_sequences_grow():
+    """Contexts crossing the 256- and 512-token bounds pick larger-grid graphs; logits stay eager's."""
+    model = _model(seed=7)
+    r_e, bm_e = _runner(model, num_blocks=256)
+    r_g, bm_g = _runner(model, num_blocks=256)
+    from nanoserve_amd.engine import DecodeGraphs
+    r_g.graphs = DecodeGraphs(r_g, (1, 2, 4), max_model_len=1024)
+    assert r_g.graphs.ctx_sizes == [256, 512, 1024]
+    prompts = [_tokens(n, 512, 500 + n) for n in (250, 509, 40)]
+    se = [_seq(i, p, max_new=64) for i, p in enumerate(prompts)]
+    sg = [_seq(i, p, max_new=64) for i, p in enumerate(prompts)]
+    logits, *_ = _step(r_e, bm_e, [(s, s.prompt_len) for s in se])
+    _step(r_g, bm_g, [(s, s.prompt_len) for s in sg])
+    toks = logits.argmax(-1).tolist()
+    used = set()
+    for step in range(8):
+        for a, b_, t in zip(se, sg, toks):
+            a.output_token_ids.append(t)
+            b_.output_token_ids.append(t)
+        want, *_ = _step(r_e, bm_e, [(s, 1) for s in se])
+        for s in sg:
+            assert bm_g.allocate(s, s.num_computed_tokens + 1)
+        longest = max(s.num_computed_tokens + 1 for s in sg)
+        used.add(next(c for c in r_g.graphs.ctx_sizes if c >= longest))
+        with torch.inference_mode():
+            r_g.execute([(s, 1) for s in sg])
+        got = r_g.graphs.last_logits
+        torch.cuda.synchronize()
+        assert relative_error(got, want) < TOL, f"step {step}"
+        toks = want.argmax(-1).tolist()
+    assert used == {512, 1024}
