@@ -78,33 +78,37 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   using V8 = typename DT::vec8;
   using T = typename DT::T;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // Uniform per wave: the chunk split below then branches on scalars, and
+  // the compiler does not treat the batch paths as divergent (which made it
+  // wait for every load in flight where they join).
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int n0 = blockIdx.x * 16;
   const int m0 = blockIdx.y * MT;
   const int row = lane & 15;  // A row (feature) / B column (token) of this lane
   const int grp = lane >> 4;  // lane group: k-slots 8*grp .. +7 of an MFMA step
   const int nf = n0 + 4 * grp; // first of the four output features this lane ends with
 
-  // The epilogue's inputs are fetched first so their latency hides behind the K loop.
-  float bias[4] = {0.f, 0.f, 0.f, 0.f};
-  float resid[NT][4];
+  // The epilogue's inputs are fetched first so their latency hides behind the
+  // K loop.  They stay in the model dtype until the epilogue: converting them
+  // here would make the wave wait for them before issuing any weight load.
+  T bias_raw[4] = {T(0.f), T(0.f), T(0.f), T(0.f)};
+  typename DT::vec4 resid_raw[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) resid_raw[t][r] = T(0.f);
   if (wave == 0) {
     if (p.bias) {
       const T* bp = static_cast<const T*>(p.bias) + nf;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(bp[r]);
+      for (int r = 0; r < 4; ++r) bias_raw[r] = bp[r];
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const int m = m0 + 16 * t + row;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) resid[t][r] = 0.f;
-      if (p.epilogue == NS_EPILOGUE_RESIDUAL && m < p.M) {
-        const typename DT::vec4 rv = *reinterpret_cast<const typename DT::vec4*>(
+      if (p.epilogue == NS_EPILOGUE_RESIDUAL && m < p.M)
+        resid_raw[t] = *reinterpret_cast<const typename DT::vec4*>(
             static_cast<const T*>(p.residual) + static_cast<int64_t>(m) * p.N + nf);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) resid[t][r] = from_model<DT>(rv[r]);
-      }
     }
   }
 
@@ -136,15 +140,17 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
       const u32x4 codes = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
       const int gi = kb / p.group_size;
       const float scale = srow[gi];
-      const float zero = static_cast<float>(zrow[gi]);
+      const uint32_t zq = zrow[gi];  // converted after the x loads are issued
       V8 b[4][NT], nw[4];
+      // Rows past M read row 0 (unconditional loads, no wait between them);
+      // their sums and products only reach outputs that are never stored.
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         nw[j] = load16<DT>(static_cast<const char*>(p.norm_weight) + (kb + 8 * j) * ESZ);
 #pragma unroll
-        for (int t = 0; t < NT; ++t)
-          b[j][t] = xok[t] ? load16<DT>(xrow[t] + (kb + 8 * j) * ESZ) : zero8<DT>();
+        for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
       }
+      __builtin_amdgcn_sched_barrier(0);
       __shared__ float nss[WAVES][NT][16];
       float ss[NT];
 #pragma unroll
@@ -174,6 +180,7 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
           for (int e = 0; e < 8; ++e)
             b[j][t][e] = to_model<DT>(static_cast<float>(b[j][t][e]) * rstd * static_cast<float>(nw[j][e]));
       }
+      const float zero = static_cast<float>(zq);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const V8 a = dequant8<DT>(codes[j], zero, scale);
@@ -183,40 +190,77 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
   }
 
-  // Whole 128-wide chunks, split between the waves; each wave fetches the
-  // codes, scales and zeros of up to BATCH chunks before using any of them.
+  // Whole 128-wide chunks, split between the waves.
   const int chunks = p.norm_weight ? 0 : p.K / 128;
+  const int c_beg = (chunks * wave) / WAVES;
   const int c_end = (chunks * (wave + 1)) / WAVES;
-  for (int c0 = (chunks * wave) / WAVES; c0 < c_end; c0 += BATCH) {
-    const int nb = c_end - c0 < BATCH ? c_end - c0 : BATCH;
-    u32x4 codes[BATCH];
-    float scale[BATCH], zero[BATCH];
+  if constexpr (BATCH == 1) {
+    // One chunk per wave (K up to 8 chunks): the chunk's codes, scale, zero
+    // point and x operands are all issued before any of them is used, so the
+    // wave makes one memory round trip.  The zero point stays a raw byte
+    // until then (converting it at its load made the wave wait for that
+    // load before issuing the next), and rows past M read row 0, whose
+    // products only reach outputs that are never stored (no branch, so no
+    // wait, between loads).
+    for (int c = c_beg; c < c_end; ++c) {
+      const int kb = 128 * c + 32 * grp;
+      const u32x4 codes = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
+      const int gi = kb / p.group_size;
+      const float scale = srow[gi];
+      const uint32_t zq = zrow[gi];
+      V8 b[4][NT];
 #pragma unroll
-    for (int i = 0; i < BATCH; ++i) {
-      if (i < nb) {
-        const int kb = 128 * (c0 + i) + 32 * grp;
-        codes[i] = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
-        const int gi = kb / p.group_size;
-        scale[i] = srow[gi];
-        zero[i] = static_cast<float>(zrow[gi]);
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
+      // Loads complete in order: keep them all ahead of the arithmetic.
+      __builtin_amdgcn_sched_barrier(0);
+      const float zero = static_cast<float>(zq);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const V8 a = dequant8<DT>(codes[j], zero, scale);
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
       }
     }
+  } else {
+    // Several chunks per wave (down_proj's K = 4864): the codes, scales and
+    // zero points of up to BATCH chunks are fetched first, the x operands
+    // chunk by chunk.  Issuing every chunk's x at once measured slower
+    // (M = 16..64: 8.4 -> 12.3 us): a 16-row load uses half of each line it
+    // touches, and with all chunks in flight the lines leave L1 before the
+    // load that uses their other half.
+    for (int c0 = c_beg; c0 < c_end; c0 += BATCH) {
+      const int nb = c_end - c0 < BATCH ? c_end - c0 : BATCH;
+      u32x4 codes[BATCH];
+      float scale[BATCH], zero[BATCH];
 #pragma unroll
-    for (int i = 0; i < BATCH; ++i) {
-      if (i < nb) {
-        const int kb = 128 * (c0 + i) + 32 * grp;
-        V8 b[4][NT];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-#pragma unroll
-          for (int t = 0; t < NT; ++t)
-            b[j][t] = xok[t] ? load16<DT>(xrow[t] + (kb + 8 * j) * ESZ) : zero8<DT>();
+      for (int i = 0; i < BATCH; ++i) {
+        if (i < nb) {
+          const int kb = 128 * (c0 + i) + 32 * grp;
+          codes[i] = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
+          const int gi = kb / p.group_size;
+          scale[i] = srow[gi];
+          zero[i] = static_cast<float>(zrow[gi]);
         }
+      }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const V8 a = dequant8<DT>(codes[i][j], zero[i], scale[i]);
+      for (int i = 0; i < BATCH; ++i) {
+        if (i < nb) {
+          const int kb = 128 * (c0 + i) + 32 * grp;
+          V8 b[4][NT];
 #pragma unroll
-          for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+          for (int j = 0; j < 4; ++j) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+              b[j][t] = xok[t] ? load16<DT>(xrow[t] + (kb + 8 * j) * ESZ) : zero8<DT>();
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const V8 a = dequant8<DT>(codes[i][j], zero[i], scale[i]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+          }
         }
       }
     }
@@ -252,6 +296,9 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 
   // D[4·(lane/16) + r][lane%16]: features nf .. nf+3 of token m.  Each
   // epilogue rounds where the reference's separate tensor ops round.
+  float bias[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(bias_raw[r]);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int m = m0 + 16 * t + row;
@@ -274,7 +321,7 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
     typename DT::vec4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + resid[t][r]);
+    for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + from_model<DT>(resid_raw[t][r]));
     *reinterpret_cast<typename DT::vec4*>(static_cast<T*>(p.out) + static_cast<int64_t>(m) * p.N + nf) = o;
   }
 }
