@@ -45,6 +45,10 @@ class SchedulerConfig:
     max_num_batched_tokens: int = 2048
     max_num_seqs: int = 64
     enable_chunked_prefill: bool = True
+    # "recompute": evict the newest running sequence and re-prefill it later;
+    # "none": running out of KV blocks raises instead of stalling (the
+    # reference's ablation mode, config.py:82, scheduler.py:205-252).
+    preemption_mode: str = "recompute"
 
 
 class SeqStatus(enum.Enum):
@@ -155,18 +159,43 @@ class Sequence:
 class SchedulerOutput:
     scheduled: list = field(default_factory=list)  # [(Sequence, num_tokens)]
     preempted: list = field(default_factory=list)
+    num_batched_tokens: int = 0
+    num_prefill_seqs: int = 0
+    num_decode_seqs: int = 0
 
     def __bool__(self) -> bool:
         return bool(self.scheduled)
 
 
+@dataclass
+class SchedulerStats:
+    """Running totals over the scheduler's life (reference scheduler.py:55-66)."""
+
+    total_steps: int = 0
+    total_preemptions: int = 0
+    total_prefill_tokens: int = 0
+    total_decode_tokens: int = 0
+    batch_size_sum: int = 0
+    mixed_steps: int = 0
+
+    @property
+    def mean_batch_size(self) -> float:
+        return self.batch_size_sum / self.total_steps if self.total_steps else 0.0
+
+
 class Scheduler:
     def __init__(self, cfg: SchedulerConfig, block_manager: BlockSpaceManager) -> None:
+        if cfg.preemption_mode not in ("recompute", "none"):
+            raise ValueError(f"unknown preemption_mode {cfg.preemption_mode!r}")
         self.cfg = cfg
         self.block_manager = block_manager
         self.waiting: deque[Sequence] = deque()
         self.running: list[Sequence] = []
-        self.num_preemptions = 0
+        self.stats = SchedulerStats()
+
+    @property
+    def num_preemptions(self) -> int:
+        return self.stats.total_preemptions
 
     def add(self, seq: Sequence) -> None:
         seq.status = SeqStatus.WAITING
@@ -180,6 +209,20 @@ class Scheduler:
         out = SchedulerOutput()
         budget = self._schedule_running(out, self.cfg.max_num_batched_tokens)
         self._schedule_waiting(out, budget)
+        # Counted before the runner advances num_computed_tokens, while
+        # is_prefilling still says what this step does for each sequence.
+        for seq, q in out.scheduled:
+            if seq.is_prefilling:
+                out.num_prefill_seqs += 1
+                self.stats.total_prefill_tokens += q
+            else:
+                out.num_decode_seqs += 1
+                self.stats.total_decode_tokens += q
+            out.num_batched_tokens += q
+        if out.scheduled:
+            self.stats.total_steps += 1
+            self.stats.batch_size_sum += len(out.scheduled)
+            self.stats.mixed_steps += bool(out.num_prefill_seqs and out.num_decode_seqs)
         return out
 
     def _schedule_running(self, out: SchedulerOutput, budget: int) -> int:
@@ -201,14 +244,20 @@ class Scheduler:
             need = seq.num_computed_tokens + want
             admitted = True
             while not self.block_manager.allocate(seq, need):
-                victim = next((s for s in reversed(snapshot)
-                               if s.status is SeqStatus.RUNNING and s.seq_id not in protected and s is not seq),
-                              None)
+                victim = None if self.cfg.preemption_mode == "none" else next(
+                    (s for s in reversed(snapshot)
+                     if s.status is SeqStatus.RUNNING and s.seq_id not in protected and s is not seq), None)
                 if victim is None:
                     cap = self.block_manager.num_total_blocks - self.block_manager.watermark_blocks
                     if self.block_manager.blocks_for(need) > cap:
                         raise ValueError(f"request {seq.seq_id} needs {self.block_manager.blocks_for(need)} "
                                          f"KV blocks but the cache holds {cap}")
+                    if self.cfg.preemption_mode == "none":
+                        # Without eviction nothing can free a block: say so
+                        # rather than stall (reference scheduler.py:222-252).
+                        raise RuntimeError(f"out of KV blocks at request {seq.seq_id} with preemption disabled: "
+                                           f"{len(snapshot)} running sequences hold all "
+                                           f"{self.block_manager.num_total_blocks} blocks")
                     # Last one standing: it goes back to the queue and retries.
                     self._preempt(seq, out)
                     admitted = False
@@ -254,7 +303,7 @@ class Scheduler:
         """Newest-first eviction by recompute: free the blocks, requeue at the front."""
         self.block_manager.free(seq)
         seq.reset_for_recompute()
-        self.num_preemptions += 1
+        self.stats.total_preemptions += 1
         out.preempted.append(seq)
         self.waiting.appendleft(seq)
 

@@ -7,7 +7,12 @@ reference forward in float32.  Bounds: logits within 1e-2 of the oracle's
 (max |diff| / max |oracle|, fp16 activations rounded after every op), and the
 reference's model properties (tests/test_model.py:54-136) within the same
 bound: incremental decode == one-shot prefill, chunked == one-shot, and a
-sequence's logits independent of its batchmates.
+sequence's logits independent of its batchmates.  The engine's integration
+properties (tests/test_integration.py:38-166) -- chunked prefill, preemption,
+one request at a time and requests added mid-flight -- are checked as: every
+request ends with its length, no block leaks, every emitted token is the
+model's greedy choice under a teacher-forced replay (fp16 near-ties aside),
+and nine in ten tokens match the plain run.
 """
 
 from __future__ import annotations
@@ -265,3 +270,71 @@ def test_decode_graphs_switch_context_buckets_as_sequences_grow():
         assert relative_error(got, want) < TOL, f"step {step}"
         toks = want.argmax(-1).tolist()
     assert used == {512, 1024}
+
+
+# ---- engine integration (reference tests/test_integration.py:38-166) -------------
+_LENS = [(5, 6), (33, 3), (17, 9), (70, 4), (2, 12), (40, 7)]
+
+
+@torch.inference_mode()
+def _teacher_forced_logits(model, tokens):
+    """Logits of every position of `tokens`, one-shot prefill into a fresh cache."""
+    runner, bm = _runner(model, num_blocks=64, block_size=8)
+    s = _seq(0, tokens)
+    assert bm.allocate(s, len(tokens))
+    ids, pos, md, _, _ = runner.build_inputs([(s, len(tokens))])
+    hidden = runner.model(ids, pos, runner.kv_cache, md, runner.attn_fn)
+    return runner.model.compute_logits(hidden, torch.arange(len(tokens), device=DEV)).float()
+
+
+def _assert_greedy(model, seq):
+    """Every generated token is the model's argmax at its position, up to fp16 near-ties."""
+    full = seq.prompt_token_ids + seq.output_token_ids
+    logits = _teacher_forced_logits(model, full[:-1])
+    rows = logits[seq.prompt_len - 1:]
+    picked = rows.gather(1, torch.tensor(seq.output_token_ids, device=DEV)[:, None])[:, 0]
+    gap = rows.max(dim=1).values - picked
+    assert float(gap.max()) <= 5 * TOL * float(rows.abs().max()), (seq.seq_id, gap.tolist())
+
+
+def _run_engine(model, mode):
+    budget, max_seqs, blocks = {"plain": (512, 8, 128), "chunked": (16, 8, 128), "preempting": (64, 8, 14),
+                                "one_at_a_time": (512, 1, 128), "mid_flight": (64, 8, 128)}[mode]
+    eng = LLMEngine(model, num_blocks=blocks, block_size=8, device=DEV,
+                    scheduler_config=SchedulerConfig(max_num_batched_tokens=budget, max_num_seqs=max_seqs),
+                    max_model_len=256)
+    reqs = [(_tokens(p, 512, 700 + i), SamplingParams(max_new_tokens=n, ignore_eos=True))
+            for i, (p, n) in enumerate(_LENS)]
+    if mode == "mid_flight":
+        for r in reqs[:3]:
+            eng.add_request(*r)
+        out = []
+        for _ in range(4):
+            out += eng.step()
+        for r in reqs[3:]:
+            eng.add_request(*r)
+        while eng.has_unfinished_requests:
+            out += eng.step()
+        out.sort(key=lambda s: s.seq_id)
+    else:
+        for r in reqs:
+            eng.add_request(*r)
+        out = eng.run_all()
+    return out, eng
+
+
+@pytest.mark.parametrize("mode", ["chunked", "preempting", "one_at_a_time", "mid_flight"])
+def test_engine_serves_every_request_greedily_however_it_is_batched(mode):
+    model = _model(seed=8)
+    plain, _ = _run_engine(model, "plain")
+    out, eng = _run_engine(model, mode)
+    assert [len(s.output_token_ids) for s in out] == [n for _, n in _LENS]
+    assert eng.block_manager.num_free_blocks == eng.block_manager.num_total_blocks  # nothing leaked
+    if mode == "preempting":
+        assert eng.scheduler.num_preemptions > 0
+    if mode == "chunked":
+        assert eng.scheduler.stats.mixed_steps > 0
+    for s in out:
+        _assert_greedy(model, s)
+    same = sum(a == b for x, y in zip(plain, out) for a, b in zip(x.output_token_ids, y.output_token_ids))
+    assert same >= 0.9 * sum(n for _, n in _LENS), f"{same} tokens agree with the plain run"
