@@ -188,6 +188,40 @@ def test_first_greedy_token_matches_oracle_when_not_a_near_tie():
     assert checked >= 1
 
 
+def test_decode_logits_do_not_depend_on_a_prefilling_batchmate():
+    """One sequence decoding beside another's prefill in a mixed batch (reference
+    tests/test_model.py:99-126): the decoding row's logits are those of the step alone."""
+    model = _model(seed=9)
+    a, b = _tokens(9, 512, 31), _tokens(17, 512, 32)
+
+    def decode_of_a(with_neighbour):
+        runner, bm = _runner(model)
+        sa = _seq(0, a)
+        logits, *_ = _step(runner, bm, [(sa, len(a))])
+        sa.output_token_ids.append(int(logits[0].argmax()))
+        plan = [(sa, 1)] + ([(_seq(1, b), len(b))] if with_neighbour else [])
+        logits, seqs, *_ = _step(runner, bm, plan)
+        return logits[seqs.index(sa)]
+
+    assert relative_error(decode_of_a(True), decode_of_a(False)) < TOL
+
+
+def test_block_size_does_not_change_logits():
+    """Prefill chunks and decode steps over caches of 4- to 32-token blocks give the
+    same logits (reference tests/test_model.py:129-136)."""
+    model = _model(seed=10)
+    tokens = _tokens(37, 512, 33)
+    outs = []
+    for bs in (4, 8, 16, 32):
+        runner, bm = _runner(model, num_blocks=256 // bs, block_size=bs)
+        s = _seq(0, tokens)
+        for q in (10, 1, 1, 25):
+            logits, *_ = _step(runner, bm, [(s, q)])
+        outs.append(logits[0])
+    for o in outs[1:]:
+        assert relative_error(o, outs[0]) < TOL
+
+
 @pytest.mark.parametrize("batch", [3, 8])
 def test_decode_graph_replays_match_eager_steps(batch):
     """Decode steps replayed from the captured graph (padded to a bucket) give the eager step's logits."""
