@@ -431,8 +431,16 @@ class DecodeGraphs:
                                 | {max_model_len})
         n = max(self.sizes)
         self._per = 4 * n + n * self.width  # ids, pos, slots, lens, tables
-        self._host = torch.empty(self._per, dtype=torch.int64, pin_memory=runner.device.type == "cuda")
+        self._host = torch.zeros(self._per, dtype=torch.int64, pin_memory=runner.device.type == "cuda")
+        self._host_np = self._host.numpy()
         self._dev = torch.zeros(self._per, dtype=torch.int64, device=runner.device)
+        # What each table row of the pinned buffer holds: (table width, and per
+        # row the block_table list written there and how many of its entries).
+        # Tables only grow in place (BlockSpaceManager.allocate extends the
+        # list; free installs a new one), so a row holding the same list keeps
+        # valid entries and a decode step writes only blocks added since.
+        # Holding the lists keeps their ids from reuse.
+        self._rows: tuple[int, list[tuple[list, int]]] = (0, [])
         self._graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.last_logits: torch.Tensor | None = None  # graph-owned logits of the latest replay
         self._pool = None
@@ -442,36 +450,65 @@ class DecodeGraphs:
         return (len(scheduled) <= self.sizes[-1] and all(q == 1 for _, q in scheduled)
                 and all(s.num_tokens <= self.max_model_len for s, _ in scheduled))
 
-    def _views(self, b: int):
-        n = max(self.sizes)
+    def _table_width(self, ctx: int) -> int:
+        return -(-ctx // self.runner.block_size)
+
+    def _views(self, b: int, ctx: int):
+        n, w = max(self.sizes), self._table_width(ctx)
         d = self._dev
         return (d[0:b], d[n:n + b], d[2 * n:2 * n + b], d[3 * n:3 * n + b],
-                d[4 * n:4 * n + b * self.width].view(b, self.width))
+                d[4 * n:4 * n + b * w].view(b, w))
 
     def _metadata(self, b: int, ctx: int) -> tuple[torch.Tensor, torch.Tensor, AttentionMetadata]:
-        ids, pos, slots, lens, tables = self._views(b)
+        ids, pos, slots, lens, tables = self._views(b, ctx)
         md = AttentionMetadata(
             slot_mapping=slots, query_start_loc=None, seq_lens=lens, block_tables=tables,
             max_query_len=1, max_seq_len=ctx, num_seqs=b, num_tokens=b,
             is_decode_only=True, query_lens_cpu=None, seq_lens_cpu=None, query_start_loc_cpu=None)
         return ids, pos, md
 
-    def _fill(self, scheduled, b: int) -> None:
-        n = max(self.sizes)
-        h = np.zeros(self._per, dtype=np.int64)
-        h[2 * n:2 * n + b] = -1  # padding rows write no cache slot
-        h[3 * n:3 * n + b] = 1
-        bs, w = self.runner.block_size, self.width
+    def _fill(self, scheduled, b: int, ctx: int) -> None:
+        """Write the step's inputs for rows [0, b) and copy them to the device.
+
+        Only what the graph reads is written: each row's token, position,
+        slot and length, and its block-table entries up to its length
+        (entries past a row's length are never read, so stale ones stay);
+        padding rows get slot -1 (no cache write), length 1 and block 0."""
+        n, bs, w = max(self.sizes), self.runner.block_size, self._table_width(ctx)
+        h = self._host_np
+        ids, pos, slots, lens = h[0:n], h[n:2 * n], h[2 * n:3 * n], h[3 * n:4 * n]
+        tab = h[4 * n:4 * n + b * w].reshape(b, w)
+        k = len(scheduled)
+        ids[k:b] = 0
+        pos[k:b] = 0
+        slots[k:b] = -1
+        lens[k:b] = 1
+        tab[k:b, 0] = 0
+        prev = self._rows[1] if self._rows[0] == w else []
+        rows = []
+        tok, at, slot = [], [], []
         for i, (seq, _) in enumerate(scheduled):
             p = seq.num_computed_tokens
-            h[i] = seq.slice_token_ids(p, p + 1)[0]
-            h[n + i] = p
-            h[2 * n + i] = seq.block_table[p // bs] * bs + p % bs
-            h[3 * n + i] = p + 1
-            row = seq.block_table[:w]
-            h[4 * n + i * w:4 * n + i * w + len(row)] = row
-        self._host.copy_(torch.from_numpy(h))
-        self._dev.copy_(self._host)  # ordered before the replay on the same stream
+            plen = len(seq.prompt_token_ids)
+            bt = seq.block_table
+            tok.append(seq.output_token_ids[p - plen] if p >= plen else seq.prompt_token_ids[p])
+            at.append(p)
+            slot.append(bt[p // bs] * bs + p % bs)
+            nb = p // bs + 1
+            have = prev[i][1] if i < len(prev) and prev[i][0] is bt else 0
+            if nb > have:
+                tab[i, have:nb] = bt[have:nb]
+            rows.append((bt, max(nb, have)))
+        self._rows = (w, rows)
+        ids[:k] = tok
+        pos[:k] = at
+        slots[:k] = slot
+        lens[:k] = at
+        lens[:k] += 1
+        end = 4 * n + b * w
+        # Asynchronous: execute() reads the step's tokens back before any
+        # later fill can overwrite the pinned buffer.
+        self._dev[:end].copy_(self._host[:end], non_blocking=True)
 
     def _capture(self, b: int, ctx: int):
         r = self.runner
@@ -513,7 +550,7 @@ class DecodeGraphs:
         if (b, ctx) not in self._graphs:
             self.capture_all()
         g, out, logits = self._graphs[(b, ctx)]
-        self._fill(scheduled, b)
+        self._fill(scheduled, b, ctx)
         g.replay()
         self.last_logits = logits[:len(scheduled)]
         tokens = out[:len(scheduled)].tolist()
