@@ -418,8 +418,14 @@ class DecodeGraphs:
     at once.  Graphs are therefore also keyed by a context bucket (powers of
     two up to max_model_len): sizing the grid for 4096 tokens when the batch's
     longest context is under 1024 doubles the attention time (MI355X, 32
-    sequences: 18.9 us against 9.5 us).  The block tables always have
-    max_model_len / block_size columns.
+    sequences: 18.9 us against 9.5 us).  Each graph's block table has its
+    context bucket's width.
+
+    `launch` and `tokens` split a step so that the engine can plan and launch
+    the next step before reading this one's tokens back: the next step's input
+    ids are then gathered on the device from this step's greedy output.  Two
+    pinned staging buffers alternate, so filling step N+1 never overwrites the
+    buffer step N's copy may still be reading.
     """
 
     def __init__(self, runner: "ModelRunner", sizes: tuple[int, ...], max_model_len: int) -> None:
@@ -430,17 +436,20 @@ class DecodeGraphs:
         self.ctx_sizes = sorted({max_model_len >> k for k in range(4) if (max_model_len >> k) >= 256}
                                 | {max_model_len})
         n = max(self.sizes)
-        self._per = 4 * n + n * self.width  # ids, pos, slots, lens, tables
-        self._host = torch.zeros(self._per, dtype=torch.int64, pin_memory=runner.device.type == "cuda")
-        self._host_np = self._host.numpy()
+        self._per = 5 * n + n * self.width  # ids, pos, slots, lens, gather rows, tables
+        pin = runner.device.type == "cuda"
+        self._host = [torch.zeros(self._per, dtype=torch.int64, pin_memory=pin) for _ in range(2)]
+        self._host_np = [h.numpy() for h in self._host]
+        self._tok = [torch.zeros(n, dtype=torch.int64, pin_memory=pin) for _ in range(2)]
+        self._next = 0  # staging buffer of the next launch
         self._dev = torch.zeros(self._per, dtype=torch.int64, device=runner.device)
-        # What each table row of the pinned buffer holds: (table width, and per
+        # What each table row of a staging buffer holds: (table width, and per
         # row the block_table list written there and how many of its entries).
         # Tables only grow in place (BlockSpaceManager.allocate extends the
         # list; free installs a new one), so a row holding the same list keeps
         # valid entries and a decode step writes only blocks added since.
         # Holding the lists keeps their ids from reuse.
-        self._rows: tuple[int, list[tuple[list, int]]] = (0, [])
+        self._rows: list[tuple[int, list[tuple[list, int]]]] = [(0, []), (0, [])]
         self._graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
         self.last_logits: torch.Tensor | None = None  # graph-owned logits of the latest replay
         self._pool = None
@@ -457,7 +466,7 @@ class DecodeGraphs:
         n, w = max(self.sizes), self._table_width(ctx)
         d = self._dev
         return (d[0:b], d[n:n + b], d[2 * n:2 * n + b], d[3 * n:3 * n + b],
-                d[4 * n:4 * n + b * w].view(b, w))
+                d[5 * n:5 * n + b * w].view(b, w))
 
     def _metadata(self, b: int, ctx: int) -> tuple[torch.Tensor, torch.Tensor, AttentionMetadata]:
         ids, pos, slots, lens, tables = self._views(b, ctx)
@@ -467,24 +476,30 @@ class DecodeGraphs:
             is_decode_only=True, query_lens_cpu=None, seq_lens_cpu=None, query_start_loc_cpu=None)
         return ids, pos, md
 
-    def _fill(self, scheduled, b: int, ctx: int) -> None:
-        """Write the step's inputs for rows [0, b) and copy them to the device.
+    def _fill(self, scheduled, b: int, ctx: int, gather: list[int] | None) -> int:
+        """Write the step's inputs for rows [0, b) into the next staging buffer
+        and copy them to the device; returns the staging buffer used.
 
         Only what the graph reads is written: each row's token, position,
         slot and length, and its block-table entries up to its length
         (entries past a row's length are never read, so stale ones stay);
-        padding rows get slot -1 (no cache write), length 1 and block 0."""
+        padding rows get slot -1 (no cache write), length 1 and block 0.
+        With `gather`, row i's token is not known on the host yet and is row
+        gather[i] of the previous launch's greedy output."""
         n, bs, w = max(self.sizes), self.runner.block_size, self._table_width(ctx)
-        h = self._host_np
-        ids, pos, slots, lens = h[0:n], h[n:2 * n], h[2 * n:3 * n], h[3 * n:4 * n]
-        tab = h[4 * n:4 * n + b * w].reshape(b, w)
+        slot_i = self._next
+        self._next ^= 1
+        h = self._host_np[slot_i]
+        ids, pos, slots, lens, rows_src = h[0:n], h[n:2 * n], h[2 * n:3 * n], h[3 * n:4 * n], h[4 * n:5 * n]
+        tab = h[5 * n:5 * n + b * w].reshape(b, w)
         k = len(scheduled)
         ids[k:b] = 0
         pos[k:b] = 0
         slots[k:b] = -1
         lens[k:b] = 1
         tab[k:b, 0] = 0
-        prev = self._rows[1] if self._rows[0] == w else []
+        width, prev = self._rows[slot_i]
+        prev = prev if width == w else []
         rows = []
         tok, at, slot = [], [], []
         for i, (seq, _) in enumerate(scheduled):
@@ -499,16 +514,20 @@ class DecodeGraphs:
             if nb > have:
                 tab[i, have:nb] = bt[have:nb]
             rows.append((bt, max(nb, have)))
-        self._rows = (w, rows)
-        ids[:k] = tok
+        self._rows[slot_i] = (w, rows)
+        ids[:k] = tok if gather is None else 0
         pos[:k] = at
         slots[:k] = slot
         lens[:k] = at
         lens[:k] += 1
-        end = 4 * n + b * w
-        # Asynchronous: execute() reads the step's tokens back before any
-        # later fill can overwrite the pinned buffer.
-        self._dev[:end].copy_(self._host[:end], non_blocking=True)
+        if gather is not None:
+            rows_src[:k] = gather
+        end = 5 * n + b * w
+        # Asynchronous: this staging buffer is written again two launches
+        # later, after the engine has read back the tokens of the launch in
+        # between, which comes after this copy on the stream.
+        self._dev[:end].copy_(self._host[slot_i][:end], non_blocking=True)
+        return slot_i
 
     def _capture(self, b: int, ctx: int):
         r = self.runner
@@ -542,21 +561,55 @@ class DecodeGraphs:
                 if (b, ctx) not in self._graphs:
                     self._capture(b, ctx)
 
-    def execute(self, scheduled) -> list[tuple[Sequence, int]]:
-        r = self.runner
+    @torch.inference_mode()
+    def launch(self, scheduled, after: "GraphLaunch | None" = None) -> "GraphLaunch":
+        """Replay the step's graph; with `after`, every row's token comes from
+        that earlier launch's greedy output (gathered on the device)."""
         b = next(x for x in self.sizes if x >= len(scheduled))
         longest = max(seq.num_computed_tokens + 1 for seq, _ in scheduled)
         ctx = next(c for c in self.ctx_sizes if c >= longest)
         if (b, ctx) not in self._graphs:
             self.capture_all()
         g, out, logits = self._graphs[(b, ctx)]
-        self._fill(scheduled, b, ctx)
+        gather = None
+        if after is not None:
+            where = {seq.seq_id: i for i, (seq, _) in enumerate(after.scheduled)}
+            gather = [where[seq.seq_id] for seq, _ in scheduled]
+        slot_i = self._fill(scheduled, b, ctx, gather)
+        k = len(scheduled)
+        if after is not None:
+            n = max(self.sizes)
+            torch.index_select(after.out, 0, self._dev[4 * n:4 * n + k], out=self._dev[0:k])
         g.replay()
-        self.last_logits = logits[:len(scheduled)]
-        tokens = out[:len(scheduled)].tolist()
+        self.last_logits = logits[:k]
+        # The tokens leave the graph's output before a later replay of the
+        # same graph can overwrite it.
+        tok = self._tok[slot_i]
+        tok[:k].copy_(out[:k], non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+        return GraphLaunch(list(scheduled), out, tok, done)
+
+    def tokens(self, launch: "GraphLaunch") -> list[int]:
+        launch.done.synchronize()
+        return launch.tokens_host[:len(launch.scheduled)].tolist()
+
+    def execute(self, scheduled) -> list[tuple[Sequence, int]]:
+        launch = self.launch(scheduled)
+        tokens = self.tokens(launch)
         for seq, q in scheduled:
             seq.advance_computed(q)
         return [(seq, tok) for (seq, _), tok in zip(scheduled, tokens)]
+
+
+@dataclass
+class GraphLaunch:
+    """A replayed decode step whose tokens may not have been read back yet."""
+
+    scheduled: list
+    out: torch.Tensor          # the graph's greedy output (device)
+    tokens_host: torch.Tensor  # pinned copy of it, valid once `done` has completed
+    done: torch.cuda.Event
 
 
 class LLMEngine:
@@ -564,7 +617,7 @@ class LLMEngine:
 
     def __init__(self, model, num_blocks: int, block_size: int = 16, device="cuda",
                  scheduler_config: SchedulerConfig | None = None, eos_token_id: int | None = None,
-                 max_model_len: int = 4096, use_graphs: bool = False) -> None:
+                 max_model_len: int = 4096, use_graphs: bool = False, pipeline_decode: bool = True) -> None:
         self.model = model.eval().requires_grad_(False)
         self.device = torch.device(device)
         dtype = model.model.embed_tokens.weight.dtype
@@ -578,6 +631,9 @@ class LLMEngine:
         self.max_model_len = max_model_len
         self._next_id = 0
         self.finished: list[Sequence] = []
+        # A graph-replayed decode step whose tokens have not been read back.
+        self._inflight: GraphLaunch | None = None
+        self.pipeline_decode = pipeline_decode
 
     def add_request(self, prompt_token_ids: list[int], sampling: SamplingParams | None = None) -> int:
         sampling = sampling or SamplingParams()
@@ -590,24 +646,70 @@ class LLMEngine:
 
     @property
     def has_unfinished_requests(self) -> bool:
-        return self.scheduler.has_work
+        return self.scheduler.has_work or self._inflight is not None
 
-    def step(self) -> list[Sequence]:
-        sched = self.scheduler.schedule()
-        if not sched:
-            return []
-        results = self.runner.execute(sched.scheduled)
+    def _pipelines(self, scheduled) -> bool:
+        """A decode step can be launched before the previous step's tokens are
+        read back when it replays a graph and no sequence in it can stop on a
+        token value: stops then depend on lengths alone, so the schedule does
+        not depend on the tokens."""
+        g = self.runner.graphs
+        return (self.pipeline_decode and g is not None and g.covers(scheduled)
+                and (self.eos_token_id is None or all(s.sampling.ignore_eos for s, _ in scheduled)))
+
+    def _record(self, seq: Sequence, now: float) -> None:
+        m = seq.metrics
+        if m.first_token == 0.0:
+            m.first_token = now
+        m.output_tokens = len(seq.output_token_ids)
+        m.end = now
+
+    def _run(self, scheduled) -> list[Sequence]:
+        results = self.runner.execute(scheduled)
         now = time.perf_counter()
         for seq, tok in results:
             seq.output_token_ids.append(tok)
-            m = seq.metrics
-            if m.first_token == 0.0:
-                m.first_token = now
-            m.output_tokens = len(seq.output_token_ids)
-            m.end = now
+            self._record(seq, now)
             seq.check_stop(self.eos_token_id)
         done = self.scheduler.free_finished()
         self.finished.extend(done)
+        return done
+
+    def step(self) -> list[Sequence]:
+        """One scheduling step.  Decode steps that replay a graph are pipelined:
+        step N is launched, its sequences are advanced with placeholder tokens
+        (stops by length only), step N+1 is scheduled and launched with its
+        input ids gathered on the device from step N's output, and only then
+        are step N's tokens read back into the placeholders.  Token values and
+        order are those of the unpipelined engine."""
+        pending, self._inflight = self._inflight, None
+        done: list[Sequence] = []
+        held: list[int] = []
+        if pending is not None:
+            for seq, _ in pending.scheduled:
+                seq.advance_computed(1)
+                seq.output_token_ids.append(-1)  # placeholder until the tokens are read back
+                held.append(len(seq.output_token_ids) - 1)
+                seq.check_stop(None)
+            done = self.scheduler.free_finished()
+            self.finished.extend(done)
+        sched = self.scheduler.schedule()
+        nxt = None
+        if sched and self._pipelines(sched.scheduled):
+            if pending is None:
+                nxt = self.runner.graphs.launch(sched.scheduled)
+            elif {s.seq_id for s, _ in sched.scheduled} <= {s.seq_id for s, _ in pending.scheduled}:
+                nxt = self.runner.graphs.launch(sched.scheduled, after=pending)
+        if pending is not None:
+            tokens = self.runner.graphs.tokens(pending)
+            now = time.perf_counter()
+            for (seq, _), at, tok in zip(pending.scheduled, held, tokens):
+                seq.output_token_ids[at] = tok
+                self._record(seq, now)
+        if nxt is not None:
+            self._inflight = nxt
+        elif sched:
+            done += self._run(sched.scheduled)
         return done
 
     def run_all(self) -> list[Sequence]:

@@ -55,6 +55,9 @@ def _seq(i, tokens, max_new=4):
     return Sequence(i, list(tokens), SamplingParams(max_new_tokens=max_new, ignore_eos=True))
 
 
+_LENS = [(5, 6), (33, 3), (17, 9), (70, 4), (2, 12), (40, 7)]  # (prompt, output) lengths
+
+
 def _tokens(n, vocab, seed):
     return torch.randint(0, vocab, (n,), generator=torch.Generator().manual_seed(seed)).tolist()
 
@@ -273,6 +276,38 @@ def test_engine_with_graphs_completes_the_same_requests():
     assert same >= 0.9 * total, f"{same}/{total} tokens agree"
 
 
+@pytest.mark.parametrize("mid_flight", [False, True])
+def test_pipelined_decode_gives_the_unpipelined_tokens(mid_flight):
+    """Launching decode step N+1 before reading step N's tokens back (ids
+    gathered on the device) changes no token, no length and leaks no block."""
+    def run(pipeline):
+        model = _model(seed=11)
+        eng = LLMEngine(model, num_blocks=64, block_size=8, device=DEV,
+                        scheduler_config=SchedulerConfig(max_num_batched_tokens=64, max_num_seqs=8),
+                        max_model_len=256, use_graphs=True, pipeline_decode=pipeline)
+        reqs = [(_tokens(p, 512, 900 + i), SamplingParams(max_new_tokens=n, ignore_eos=True))
+                for i, (p, n) in enumerate(_LENS)]
+        first = reqs[:3] if mid_flight else reqs
+        for r in first:
+            eng.add_request(*r)
+        out = []
+        if mid_flight:
+            for _ in range(6):
+                out += eng.step()
+            for r in reqs[3:]:
+                eng.add_request(*r)
+        while eng.has_unfinished_requests:
+            out += eng.step()
+        out.sort(key=lambda s: s.seq_id)
+        assert eng.block_manager.num_free_blocks == 64
+        assert all(m.end >= m.first_token > 0 for m in (s.metrics for s in out))
+        return [s.output_token_ids for s in out]
+
+    plain, piped = run(False), run(True)
+    assert [len(t) for t in piped] == [n for _, n in _LENS]
+    assert piped == plain and all(t >= 0 for seq in piped for t in seq)
+
+
 def test_decode_graphs_switch_context_buckets_as_sequences_grow():
     """Contexts crossing the 256- and 512-token bounds pick larger-grid graphs; logits stay eager's."""
     model = _model(seed=7)
@@ -307,7 +342,6 @@ def test_decode_graphs_switch_context_buckets_as_sequences_grow():
 
 
 # ---- engine integration (reference tests/test_integration.py:38-166) -------------
-_LENS = [(5, 6), (33, 3), (17, 9), (70, 4), (2, 12), (40, 7)]
 
 
 @torch.inference_mode()
