@@ -15,10 +15,10 @@
 // rounded to the model dtype, exactly as dequantize_int4 computes it, so the
 // MFMA sees the reference's own dequantised weights.
 //
-// Tiling (gfx950, wave64): a workgroup owns 16 output features (one MFMA row
-// tile of W) and MT tokens (MT/16 MFMA column tiles of x^T).  K is walked in
-// chunks of 128; the workgroup's WAVES waves split the chunks between them
-// and reduce through LDS.  Within a chunk, lane group g = lane/16 owns the 32
+// Tiling (gfx950, wave64): a workgroup owns FT·16 output features (FT MFMA
+// row tiles of W, which share every x load) and MT tokens (MT/16 MFMA column
+// tiles of x^T).  K is walked in chunks of 128; the workgroup's WAVES waves
+// split the chunks between them and reduce through LDS.  Within a chunk, lane group g = lane/16 owns the 32
 // consecutive k values [128c + 32g, +32) of its feature row: one 16-byte load
 // brings all 32 codes, which feed four MFMA steps (k order permuted the same
 // way for both operands, so the sum is unchanged).  The same lane reads the
@@ -28,6 +28,10 @@
 
 namespace ns {
 namespace {
+
+// Every float op below rounds to f32 once, as the reference's separate tensor
+// ops do: no contraction into fused multiply-adds.
+#pragma clang fp contract(off)
 
 struct Int4LinearParams {
   void* out;              // [M, N] contiguous ([M, N/2] for NS_EPILOGUE_SILU_MUL), model dtype
@@ -44,8 +48,15 @@ struct Int4LinearParams {
   int M, N, K, group_size, groups;
 };
 
+// f32 -> model dtype, from a value already rounded to f32.  The empty asm
+// makes that value opaque: otherwise the backend may fold the conversion into
+// the instruction that produced it (v_fma_mixlo_f16 / v_fma_mixhi_f16 round
+// x·y straight to f16, skipping the f32 rounding in between), even with
+// contraction off and only in some instantiations, which changed the last bit
+// of dequantised weights and normalised operands between launch shapes.
 template <class DT>
 __device__ __forceinline__ typename DT::T to_model(float x) {
+  asm("" : "+v"(x));
   return static_cast<typename DT::T>(x);
 }
 
@@ -69,10 +80,16 @@ __device__ __forceinline__ typename DT::vec8 dequant8(uint32_t word, float zero,
 // SiLU in float32 as torch evaluates it for half tensors: x / (1 + exp(-x)).
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-template <class DT, int MT, int WAVES, int BATCH>
+template <class DT, int MT, int WAVES, int BATCH, int FT, bool NORM>
 __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParams p) {
   // BATCH: 128-wide chunks whose weights one wave loads at once (1 when every
   // wave has a single chunk, which keeps the register count low).
+  // FT: 16-feature row tiles per workgroup (several only with one chunk per wave).
+  // NORM: the RMSNorm prologue (p.norm_weight), in its own instantiation
+  // because its registers would lower every projection's occupancy (the
+  // 7-wave kernel needs 52 VGPRs without it, 83 with it).
+  static_assert(FT == 1 || BATCH == 1, "feature tiles need one chunk per wave");
+  static_assert(!NORM || (BATCH == 1 && FT == 1), "the RMSNorm prologue runs one chunk and one tile per wave");
   constexpr int NT = MT / 16;  // MFMA column tiles
   constexpr int ESZ = sizeof(typename DT::T);
   using V8 = typename DT::vec8;
@@ -82,40 +99,55 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   // the compiler does not treat the batch paths as divergent (which made it
   // wait for every load in flight where they join).
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * FT;
   const int m0 = blockIdx.y * MT;
   const int row = lane & 15;  // A row (feature) / B column (token) of this lane
   const int grp = lane >> 4;  // lane group: k-slots 8*grp .. +7 of an MFMA step
-  const int nf = n0 + 4 * grp; // first of the four output features this lane ends with
+  // First of the four output features this lane ends with, in row tile f: n0 + 16f + 4grp.
+  const int nf = n0 + 4 * grp;
 
   // The epilogue's inputs are fetched first so their latency hides behind the
   // K loop.  They stay in the model dtype until the epilogue: converting them
   // here would make the wave wait for them before issuing any weight load.
-  T bias_raw[4] = {T(0.f), T(0.f), T(0.f), T(0.f)};
-  typename DT::vec4 resid_raw[NT];
+  T bias_raw[FT][4];
+  typename DT::vec4 resid_raw[FT][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t)
+  for (int f = 0; f < FT; ++f) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) resid_raw[t][r] = T(0.f);
+    for (int r = 0; r < 4; ++r) bias_raw[f][r] = T(0.f);
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) resid_raw[f][t][r] = T(0.f);
+  }
   if (wave == 0) {
-    if (p.bias) {
-      const T* bp = static_cast<const T*>(p.bias) + nf;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) bias_raw[r] = bp[r];
-    }
+    for (int f = 0; f < FT; ++f) {
+      if (p.bias) {
+        const T* bp = static_cast<const T*>(p.bias) + nf + 16 * f;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int m = m0 + 16 * t + row;
-      if (p.epilogue == NS_EPILOGUE_RESIDUAL && m < p.M)
-        resid_raw[t] = *reinterpret_cast<const typename DT::vec4*>(
-            static_cast<const T*>(p.residual) + static_cast<int64_t>(m) * p.N + nf);
+        for (int r = 0; r < 4; ++r) bias_raw[f][r] = bp[r];
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int m = m0 + 16 * t + row;
+        if (p.epilogue == NS_EPILOGUE_RESIDUAL && m < p.M)
+          resid_raw[f][t] = *reinterpret_cast<const typename DT::vec4*>(
+              static_cast<const T*>(p.residual) + static_cast<int64_t>(m) * p.N + nf + 16 * f);
+      }
     }
   }
 
-  const int n = n0 + row;
-  const uint8_t* wrow = p.qweight + static_cast<int64_t>(n) * (p.K / 2);
-  const float* srow = p.scales + static_cast<int64_t>(n) * p.groups;
-  const uint8_t* zrow = p.zeros + static_cast<int64_t>(n) * p.groups;
+  const uint8_t* wrow[FT];
+  const float* srow[FT];
+  const uint8_t* zrow[FT];
+#pragma unroll
+  for (int f = 0; f < FT; ++f) {
+    const int n = n0 + 16 * f + row;
+    wrow[f] = p.qweight + static_cast<int64_t>(n) * (p.K / 2);
+    srow[f] = p.scales + static_cast<int64_t>(n) * p.groups;
+    zrow[f] = p.zeros + static_cast<int64_t>(n) * p.groups;
+  }
   const char* xrow[NT];
   bool xok[NT];
 #pragma unroll
@@ -125,73 +157,87 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     xrow[t] = p.x + static_cast<int64_t>(xok[t] ? m : 0) * p.x_stride * ESZ;
   }
 
-  floatx4 acc[NT];
+  floatx4 acc[FT][NT];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+  for (int f = 0; f < FT; ++f)
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[f][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  if constexpr (BATCH == 1) {
-    if (p.norm_weight) {
-      // RMSNorm prologue (the host guarantees one 128-wide chunk per wave):
-      // every wave already holds its slice of each x row, so the rows' sums
-      // of squares meet in LDS and the operands are scaled in registers,
-      // y = round((x * rsqrt(mean(x^2) + eps)) * w) as torch's fused
-      // rms_norm evaluates it.
-      const int kb = 128 * wave + 32 * grp;
-      const u32x4 codes = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
-      const int gi = kb / p.group_size;
-      const float scale = srow[gi];
-      const uint32_t zq = zrow[gi];  // converted after the x loads are issued
-      V8 b[4][NT], nw[4];
-      // Rows past M read row 0 (unconditional loads, no wait between them);
-      // their sums and products only reach outputs that are never stored.
+  if constexpr (NORM) {
+    // RMSNorm prologue (the host guarantees one 128-wide chunk per wave):
+    // every wave already holds its slice of each x row, so the rows' sums
+    // of squares meet in LDS and the operands are scaled in registers,
+    // y = round((x * rsqrt(mean(x^2) + eps)) * w) as torch's fused
+    // rms_norm evaluates it.
+    const int kb = 128 * wave + 32 * grp;
+    const int gi = kb / p.group_size;
+    u32x4 codes[FT];
+    float scale[FT];
+    uint32_t zq[FT];  // converted after the x loads are issued
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+      codes[f] = *reinterpret_cast<const u32x4*>(wrow[f] + kb / 2);
+      scale[f] = srow[f][gi];
+      zq[f] = zrow[f][gi];
+    }
+    V8 b[4][NT], nw[4];
+    // Rows past M read row 0 (unconditional loads, no wait between them);
+    // their sums and products only reach outputs that are never stored.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      nw[j] = load16<DT>(static_cast<const char*>(p.norm_weight) + (kb + 8 * j) * ESZ);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    __shared__ float nss[WAVES][NT][16];
+    float ss[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      ss[t] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float v = static_cast<float>(b[j][t][e]);
+          ss[t] += v * v;
+        }
+      ss[t] += __shfl_xor(ss[t], 16);  // the four lane groups holding this row
+      ss[t] += __shfl_xor(ss[t], 32);
+      if (grp == 0) nss[wave][t][row] = ss[t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) tot += nss[w][t][row];
+      const float rstd = rsqrtf(tot / static_cast<float>(p.K) + p.norm_eps);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          b[j][t][e] = to_model<DT>(static_cast<float>(b[j][t][e]) * rstd * static_cast<float>(nw[j][e]));
+    }
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+      const float zero = static_cast<float>(zq[f]);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        nw[j] = load16<DT>(static_cast<const char*>(p.norm_weight) + (kb + 8 * j) * ESZ);
+        const V8 a = dequant8<DT>(codes[f][j], zero, scale[f]);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      __shared__ float nss[WAVES][NT][16];
-      float ss[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        ss[t] = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float v = static_cast<float>(b[j][t][e]);
-            ss[t] += v * v;
-          }
-        ss[t] += __shfl_xor(ss[t], 16);  // the four lane groups holding this row
-        ss[t] += __shfl_xor(ss[t], 32);
-        if (grp == 0) nss[wave][t][row] = ss[t];
-      }
-      __syncthreads();
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        float tot = 0.f;
-#pragma unroll
-        for (int w = 0; w < WAVES; ++w) tot += nss[w][t][row];
-        const float rstd = rsqrtf(tot / static_cast<float>(p.K) + p.norm_eps);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int e = 0; e < 8; ++e)
-            b[j][t][e] = to_model<DT>(static_cast<float>(b[j][t][e]) * rstd * static_cast<float>(nw[j][e]));
-      }
-      const float zero = static_cast<float>(zq);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const V8 a = dequant8<DT>(codes[j], zero, scale);
-#pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+        for (int t = 0; t < NT; ++t) acc[f][t] = mfma16x16x32(DT{}, a, b[j][t], acc[f][t]);
       }
     }
   }
 
-  // Whole 128-wide chunks, split between the waves.
-  const int chunks = p.norm_weight ? 0 : p.K / 128;
+  // Whole 128-wide chunks, split between the waves.  The prologue has done
+  // them all when NORM is set.  Otherwise p.norm_weight is null, and testing
+  // it at run time keeps the compiler from deriving the chunk count and the
+  // tail steps from K together: with `NORM ? 0 : p.K / 128` the 7-wave kernel
+  // needed 74 VGPRs instead of 52 (two feature tiles: 128 instead of 77).
+  const bool normed = NORM || p.norm_weight != nullptr;
+  const int chunks = normed ? 0 : p.K / 128;
   const int c_beg = (chunks * wave) / WAVES;
   const int c_end = (chunks * (wave + 1)) / WAVES;
   if constexpr (BATCH == 1) {
@@ -204,10 +250,16 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     // wait, between loads).
     for (int c = c_beg; c < c_end; ++c) {
       const int kb = 128 * c + 32 * grp;
-      const u32x4 codes = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
       const int gi = kb / p.group_size;
-      const float scale = srow[gi];
-      const uint32_t zq = zrow[gi];
+      u32x4 codes[FT];
+      float scale[FT];
+      uint32_t zq[FT];
+#pragma unroll
+      for (int f = 0; f < FT; ++f) {
+        codes[f] = *reinterpret_cast<const u32x4*>(wrow[f] + kb / 2);
+        scale[f] = srow[f][gi];
+        zq[f] = zrow[f][gi];
+      }
       V8 b[4][NT];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
@@ -215,12 +267,15 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
         for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
       // Loads complete in order: keep them all ahead of the arithmetic.
       __builtin_amdgcn_sched_barrier(0);
-      const float zero = static_cast<float>(zq);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const V8 a = dequant8<DT>(codes[j], zero, scale);
+      for (int f = 0; f < FT; ++f) {
+        const float zero = static_cast<float>(zq[f]);
 #pragma unroll
-        for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+        for (int j = 0; j < 4; ++j) {
+          const V8 a = dequant8<DT>(codes[f][j], zero, scale[f]);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) acc[f][t] = mfma16x16x32(DT{}, a, b[j][t], acc[f][t]);
+        }
       }
     }
   } else {
@@ -238,10 +293,10 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
       for (int i = 0; i < BATCH; ++i) {
         if (i < nb) {
           const int kb = 128 * (c0 + i) + 32 * grp;
-          codes[i] = *reinterpret_cast<const u32x4*>(wrow + kb / 2);
+          codes[i] = *reinterpret_cast<const u32x4*>(wrow[0] + kb / 2);
           const int gi = kb / p.group_size;
-          scale[i] = srow[gi];
-          zero[i] = static_cast<float>(zrow[gi]);
+          scale[i] = srow[0][gi];
+          zero[i] = static_cast<float>(zrow[0][gi]);
         }
       }
 #pragma unroll
@@ -259,70 +314,81 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
           for (int j = 0; j < 4; ++j) {
             const V8 a = dequant8<DT>(codes[i][j], zero[i], scale[i]);
 #pragma unroll
-            for (int t = 0; t < NT; ++t) acc[t] = mfma16x16x32(DT{}, a, b[j][t], acc[t]);
+            for (int t = 0; t < NT; ++t) acc[0][t] = mfma16x16x32(DT{}, a, b[j][t], acc[0][t]);
           }
         }
       }
     }
   }
   // Remaining 32-wide steps when K is not a multiple of 128.
-  for (int s = p.norm_weight ? p.K / 32 : 4 * chunks + wave; s < p.K / 32; s += WAVES) {
+  for (int s = normed ? p.K / 32 : 4 * chunks + wave; s < p.K / 32; s += WAVES) {
     const int k = 32 * s + 8 * grp;
-    const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow + k / 2);
     const int gi = k / p.group_size;
-    const V8 a = dequant8<DT>(word, static_cast<float>(zrow[gi]), srow[gi]);
+    V8 b[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const V8 b = xok[t] ? load16<DT>(xrow[t] + k * ESZ) : zero8<DT>();
-      acc[t] = mfma16x16x32(DT{}, a, b, acc[t]);
+    for (int t = 0; t < NT; ++t) b[t] = xok[t] ? load16<DT>(xrow[t] + k * ESZ) : zero8<DT>();
+#pragma unroll
+    for (int f = 0; f < FT; ++f) {
+      const uint32_t word = *reinterpret_cast<const uint32_t*>(wrow[f] + k / 2);
+      const V8 a = dequant8<DT>(word, static_cast<float>(zrow[f][gi]), srow[f][gi]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) acc[f][t] = mfma16x16x32(DT{}, a, b[t], acc[f][t]);
     }
   }
 
   // Waves 1.. hand their partial sums to wave 0.
   if constexpr (WAVES > 1) {
-    __shared__ floatx4 red[WAVES - 1][NT][64];
+    __shared__ floatx4 red[WAVES - 1][FT][NT][64];
     if (wave > 0) {
 #pragma unroll
-      for (int t = 0; t < NT; ++t) red[wave - 1][t][lane] = acc[t];
+      for (int f = 0; f < FT; ++f)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) red[wave - 1][f][t][lane] = acc[f][t];
     }
     __syncthreads();
     if (wave != 0) return;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
+    for (int f = 0; f < FT; ++f)
 #pragma unroll
-      for (int w = 0; w < WAVES - 1; ++w) acc[t] += red[w][t][lane];
-    }
+      for (int t = 0; t < NT; ++t) {
+#pragma unroll
+        for (int w = 0; w < WAVES - 1; ++w) acc[f][t] += red[w][f][t][lane];
+      }
   }
 
-  // D[4·(lane/16) + r][lane%16]: features nf .. nf+3 of token m.  Each
-  // epilogue rounds where the reference's separate tensor ops round.
-  float bias[4];
+  // D[4·(lane/16) + r][lane%16] of row tile f: features nf+16f .. +3 of token
+  // m.  Each epilogue rounds where the reference's separate tensor ops round.
 #pragma unroll
-  for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(bias_raw[r]);
+  for (int f = 0; f < FT; ++f) {
+    const int nff = nf + 16 * f;
+    float bias[4];
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int m = m0 + 16 * t + row;
-    if (m >= p.M) continue;
-    float y[4];
+    for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(bias_raw[f][r]);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) y[r] = from_model<DT>(to_model<DT>(acc[t][r] + bias[r]));
-    if (p.epilogue == NS_EPILOGUE_SILU_MUL) {
-      // Rows (nf, nf+1) and (nf+2, nf+3) are (gate, up) pairs of outputs nf/2, nf/2+1.
-      typename DT::T o[2];
+    for (int t = 0; t < NT; ++t) {
+      const int m = m0 + 16 * t + row;
+      if (m >= p.M) continue;
+      float y[4];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const float act = from_model<DT>(to_model<DT>(silu_f32(y[2 * h])));
-        o[h] = to_model<DT>(act * y[2 * h + 1]);
+      for (int r = 0; r < 4; ++r) y[r] = from_model<DT>(to_model<DT>(acc[f][t][r] + bias[r]));
+      if (p.epilogue == NS_EPILOGUE_SILU_MUL) {
+        // Rows (nff, nff+1) and (nff+2, nff+3) are (gate, up) pairs of outputs nff/2, nff/2+1.
+        typename DT::T o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float act = from_model<DT>(to_model<DT>(silu_f32(y[2 * h])));
+          o[h] = to_model<DT>(act * y[2 * h + 1]);
+        }
+        T* dst = static_cast<T*>(p.out) + static_cast<int64_t>(m) * (p.N / 2) + nff / 2;
+        dst[0] = o[0];
+        dst[1] = o[1];
+        continue;
       }
-      T* dst = static_cast<T*>(p.out) + static_cast<int64_t>(m) * (p.N / 2) + nf / 2;
-      dst[0] = o[0];
-      dst[1] = o[1];
-      continue;
-    }
-    typename DT::vec4 o;
+      typename DT::vec4 o;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + from_model<DT>(resid_raw[t][r]));
-    *reinterpret_cast<typename DT::vec4*>(static_cast<T*>(p.out) + static_cast<int64_t>(m) * p.N + nf) = o;
+      for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + from_model<DT>(resid_raw[f][t][r]));
+      *reinterpret_cast<typename DT::vec4*>(static_cast<T*>(p.out) + static_cast<int64_t>(m) * p.N + nff) = o;
+    }
   }
 }
 
@@ -330,37 +396,54 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 // 128-wide chunk, up to 8 waves, each with a single chunk (few registers, so
 // many waves fit per SIMD).  Longer K (down_proj's 4864 = 38 chunks) gets 16
 // waves per 16-token tile (8 per 64-token tile) that each fetch up to four
-// chunks at once.
+// chunks at once.  Single-chunk waves take two feature tiles per workgroup
+// when the token tile holds at least 16 rows and the grid keeps at least 256
+// workgroups: each x operand then feeds two MFMAs, and the grid holds half as
+// many waves re-reading the token tile's x rows.  Measured on MI355X for
+// gate|up (N = 9728, K = 896), graph-replayed: 5.53 -> 5.34 us at 16 tokens,
+// 7.82 -> 7.39 at 32, 13.49 -> 11.19 at 64; at 8 tokens there is little x to
+// share and the halved grid is slower (4.67 -> 5.01 us), and four feature
+// tiles are slower than two at 32 and 64 tokens.
 struct Shape {
   int waves;
   int batch;
+  int ft;
 };
 
-Shape shape_for(int K, int mt) {
+Shape shape_for(int M, int N, int K, int mt, int mtiles, bool norm) {
   const int chunks = K / 128;
-  if (chunks >= 1 && chunks <= 8) return {chunks, 1};
-  if (K <= 2048) return {8, 4};
-  return {mt <= 16 ? 16 : 8, 4};
+  if (chunks >= 1 && chunks <= 8) {
+    const bool two = !norm && M >= 16 && N % 32 == 0 && static_cast<int64_t>(N / 32) * mtiles >= 256;
+    return {chunks, 1, two ? 2 : 1};
+  }
+  if (K <= 2048) return {8, 4, 1};
+  return {mt <= 16 ? 16 : 8, 4, 1};
+}
+
+template <class DT, int MT, int FT, bool NORM>
+const void* one_chunk_kernel(int waves) {
+  switch (waves) {
+    case 1: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 1, 1, FT, NORM>);
+    case 2: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 2, 1, FT, NORM>);
+    case 3: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 3, 1, FT, NORM>);
+    case 4: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 4, 1, FT, NORM>);
+    case 5: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 5, 1, FT, NORM>);
+    case 6: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 6, 1, FT, NORM>);
+    case 7: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 7, 1, FT, NORM>);
+    default: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 1, FT, NORM>);
+  }
 }
 
 template <class DT, int MT>
-const void* kernel_for(Shape sh) {
+const void* kernel_for(Shape sh, bool norm) {
   if (sh.batch == 1) {
-    switch (sh.waves) {
-      case 1: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 1, 1>);
-      case 2: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 2, 1>);
-      case 3: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 3, 1>);
-      case 4: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 4, 1>);
-      case 5: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 5, 1>);
-      case 6: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 6, 1>);
-      case 7: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 7, 1>);
-      default: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 1>);
-    }
+    if (norm) return one_chunk_kernel<DT, MT, 1, true>(sh.waves);
+    return sh.ft == 2 ? one_chunk_kernel<DT, MT, 2, false>(sh.waves) : one_chunk_kernel<DT, MT, 1, false>(sh.waves);
   }
   if constexpr (MT <= 16) {
-    if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4>);
+    if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4, 1, false>);
   }
-  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 4>);
+  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 4, 1, false>);
 }
 
 template <class DT>
@@ -371,9 +454,11 @@ hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
   // M = 32: down_proj 12.9 -> 8.5 us, qkv 4.1 -> 3.3 us).  Beyond that, 64-token
   // tiles amortise the dequantisation over more MFMAs.
   const int mt = p.M <= 64 ? 16 : 64;
-  const Shape sh = shape_for(p.K, mt);
-  const void* fn = mt == 16 ? kernel_for<DT, 16>(sh) : kernel_for<DT, 64>(sh);
-  const dim3 grid(static_cast<unsigned>(p.N / 16), static_cast<unsigned>((p.M + mt - 1) / mt));
+  const int mtiles = (p.M + mt - 1) / mt;
+  const bool norm = p.norm_weight != nullptr;
+  const Shape sh = shape_for(p.M, p.N, p.K, mt, mtiles, norm);
+  const void* fn = mt == 16 ? kernel_for<DT, 16>(sh, norm) : kernel_for<DT, 64>(sh, norm);
+  const dim3 grid(static_cast<unsigned>(p.N / (16 * sh.ft)), static_cast<unsigned>(mtiles));
   return hipLaunchKernel(fn, grid, dim3(64 * sh.waves), args, 0, stream);
 }
 

@@ -263,3 +263,40 @@ def test_both_methods_agree_on_every_epilogue(method):
     for a, b in zip(outs["fused"], outs["dequant"]):
         err = (a.float() - b.float()).abs()
         assert (err <= 4 * 2.0 ** -10 * b.float().abs() + 1e-3).all(), f"max err {err.max().item():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("K", [896, 928, 256])
+def test_a_row_does_not_depend_on_the_rest_of_the_batch(dtype, K):
+    """Row m's output is bit-identical whether it is launched alone or among 64 rows.
+
+    8 rows run one 16-feature tile per workgroup; 16 or more rows over a wide
+    N run two tiles that share each x load (a different grid), so this pins
+    the two-tile path bit for bit against the one-tile path on every epilogue
+    and on the 32-wide tail steps (K = 928).
+    """
+    N = 2048
+    packed, s, z = (t.to(DEV) for t in _weights(N, K, 32 if K == 928 else 128, 51))
+    gs = 32 if K == 928 else 128
+    g = torch.Generator().manual_seed(52)
+    x = torch.randn(64, K, generator=g).to(dtype).to(DEV)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype).to(DEV)
+    res = torch.randn(64, N, generator=g).to(dtype).to(DEV)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype).to(DEV)
+    cases = {"bias": {}, "residual": {"residual": None}, "silu_mul": {"silu_mul": True}}
+    if K % 128 == 0:
+        cases["rmsnorm"] = {"norm_weight": w}
+    for name, kw in cases.items():
+        def call(m):
+            args = dict(kw)
+            if "residual" in args:
+                args["residual"] = res[:m].contiguous()
+            return int4_linear(x[:m].contiguous(), packed, s, z, b, gs, **args)
+        few, many = call(8), call(64)
+        torch.cuda.synchronize()
+        assert torch.equal(few, many[:8]), f"{name}: rows differ between the 8-row and 64-row launches"
+        # The 64-row launch also stands on its own against the oracle (bias case).
+        if name == "bias":
+            wq = dequantize_int4_ref(packed.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(), gs, NAME[dtype])
+            _check(many, int4_linear_ref(x.float().cpu().numpy(), wq, b.float().cpu().numpy()), dtype,
+                   f"M=64 N={N} K={K}")
