@@ -153,6 +153,40 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                    int64_t M, int N, int K, int group_size, int dtype, void* stream);
 
 /*
+ * ns_int4_linear_rope_cache -- the q|k|v projection of one attention layer
+ * with the rotary embedding and the paged-cache write in its epilogue: one
+ * launch for what the reference runs as QuantLinear.forward of q, k and v
+ * (nanoserve/quant.py:157-158), RotaryEmbedding.apply (layers.py:84-88) and
+ * PagedKVCache.write (kv_cache.py:73-81), the steps between the layer's input
+ * and attention at reference qwen2.py:46-57.
+ *
+ * W holds the (num_heads + 2 * num_kv_heads) * head_dim rows of q, k and v
+ * in that order, in the format of ns_int4_linear, with the rows of every
+ * head in rotary-pair order: 16-row tile i of a head holds dims
+ * [8i, 8i+8) then [head_dim/2 + 8i, +8).  With y = round(x · W^T + bias)
+ * (and the RMSNorm prologue of ns_int4_linear when norm_weight is given),
+ * q and k are rotated exactly as ns_rope_reshape_and_cache rotates them;
+ * q' goes to q_out ([M, num_heads, head_dim] contiguous, original dim
+ * order), k' and v to slot_mapping's slots of k_cache / v_cache
+ * ([num_blocks, block_size, num_kv_heads, head_dim], model dtype; slots
+ * outside the cache are skipped).  Every value is bit-identical to
+ * ns_int4_linear followed by ns_rope_reshape_and_cache on the rows in
+ * original order.  cos/sin: [M, head_dim] rows, token stride
+ * cos_sin_stride_token (a multiple of 4).  K a multiple of 128 and at most
+ * 1024, head_dim a multiple of 16; q_out, the caches, cos and sin 8-byte
+ * aligned.
+ */
+int ns_int4_linear_rope_cache(void* q_out, const void* x, int64_t x_stride_row,
+                              const void* qweight, const void* scales, const void* zeros,
+                              const void* bias, const void* norm_weight, float norm_eps,
+                              const void* cos, const void* sin, int64_t cos_sin_stride_token,
+                              void* k_cache, void* v_cache,
+                              const void* slot_mapping, int slot_mapping_is_int64,
+                              int64_t M, int K, int group_size,
+                              int num_heads, int num_kv_heads, int head_dim,
+                              int block_size, int64_t num_blocks, int dtype, void* stream);
+
+/*
  * ns_int4_dequantize -- out [N, K] (`dtype`, contiguous, 16-byte aligned) =
  * the model-dtype weights of an INT4 layer: dequantize_int4 (reference
  * nanoserve/quant.py:83-95), bit for bit, in one pass.  For large token

@@ -70,6 +70,18 @@ SIGNATURES = {
         c_int64, c_int, c_int, c_int,            # M, N, K, group_size
         c_int, c_void_p,                         # dtype, stream
     ]),
+    "ns_int4_linear_rope_cache": (c_int, [
+        c_void_p, c_void_p, c_int64,             # q_out, x, x row stride
+        c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)
+        c_void_p, c_float,                       # RMSNorm weight (or None), eps
+        c_void_p, c_void_p, c_int64,             # cos, sin, token stride
+        c_void_p, c_void_p,                      # k_cache, v_cache
+        c_void_p, c_int,                         # slot_mapping, is_int64
+        c_int64, c_int, c_int,                   # M, K, group_size
+        c_int, c_int, c_int,                     # Hq, Hkv, D
+        c_int, c_int64,                          # block_size, num_blocks
+        c_int, c_void_p,                         # dtype, stream
+    ]),
     "ns_int4_dequantize": (c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p,  # out [N, K], qweight, scales, zeros
         c_int, c_int, c_int, c_int, c_void_p,    # N, K, group_size, dtype, stream

@@ -46,7 +46,27 @@ struct Int4LinearParams {
   float norm_eps;
   int epilogue;
   int M, N, K, group_size, groups;
+  // Rotary + cache-write epilogue (ROPE kernels): W's rows are q|k|v heads in
+  // rotary-pair order (rope_pair_row), out is q' [M, num_heads, head_dim].
+  const void* cos;         // [M, head_dim] rows of cs_stride elements, model dtype
+  const void* sin;
+  int64_t cs_stride;
+  void* k_cache;           // [num_slots, num_kv_heads, head_dim], model dtype
+  void* v_cache;
+  const void* slots;       // [M] int32 or int64
+  int slots64;
+  int64_t num_slots;
+  int num_heads, num_kv_heads, head_dim;
 };
+
+// Row order of a q|k|v weight for the rotary epilogue.  Within each head of
+// D rows, 16-row tile i holds dims [8i, 8i+8) then [D/2+8i, D/2+8i+8): lane
+// group g of the MFMA result then holds four dims of one half and lane group
+// g^2 (lane ^ 32) the four dims rotate_half pairs them with.  Row j of tile i
+// is this original dim:
+__host__ __device__ inline int rope_pair_dim(int i, int j, int D) {
+  return (j < 8 ? 0 : D / 2) + 8 * i + (j & 7);
+}
 
 // f32 -> model dtype, from a value already rounded to f32.  The empty asm
 // makes that value opaque: otherwise the backend may fold the conversion into
@@ -80,7 +100,7 @@ __device__ __forceinline__ typename DT::vec8 dequant8(uint32_t word, float zero,
 // SiLU in float32 as torch evaluates it for half tensors: x / (1 + exp(-x)).
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.0f + expf(-x)); }
 
-template <class DT, int MT, int WAVES, int BATCH, int FT, bool NORM>
+template <class DT, int MT, int WAVES, int BATCH, int FT, bool NORM, bool ROPE>
 __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParams p) {
   // BATCH: 128-wide chunks whose weights one wave loads at once (1 when every
   // wave has a single chunk, which keeps the register count low).
@@ -90,6 +110,9 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   // 7-wave kernel needs 52 VGPRs without it, 83 with it).
   static_assert(FT == 1 || BATCH == 1, "feature tiles need one chunk per wave");
   static_assert(!NORM || (BATCH == 1 && FT == 1), "the RMSNorm prologue runs one chunk and one tile per wave");
+  // ROPE: the epilogue rotates q and k and writes q' to out, k' and v to their
+  // cache slots (the steps between the q|k|v projection and attention).
+  static_assert(!ROPE || (BATCH == 1 && FT == 1), "the rotary epilogue runs one tile per workgroup");
   constexpr int NT = MT / 16;  // MFMA column tiles
   constexpr int ESZ = sizeof(typename DT::T);
   using V8 = typename DT::vec8;
@@ -119,6 +142,28 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int r = 0; r < 4; ++r) resid_raw[f][t][r] = T(0.f);
+  }
+  // Rotary epilogue operands (wave 0 runs the epilogue): this lane's four
+  // dims (one half of a rotary pair) of the tile's head, their cos/sin
+  // entries per token tile, and the tokens' cache slots.
+  int head = 0, dim0 = 0;
+  typename DT::vec4 cos_raw[NT], sin_raw[NT];
+  int64_t slot[NT];
+  if constexpr (ROPE) {
+    const int tiles_per_head = p.head_dim / 16;
+    head = blockIdx.x / tiles_per_head;
+    dim0 = rope_pair_dim(blockIdx.x % tiles_per_head, 4 * grp, p.head_dim);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (wave != 0) break;
+      const int m = min(m0 + 16 * t + row, p.M - 1);
+      const T* cp = static_cast<const T*>(p.cos) + static_cast<int64_t>(m) * p.cs_stride + dim0;
+      const T* sp = static_cast<const T*>(p.sin) + static_cast<int64_t>(m) * p.cs_stride + dim0;
+      cos_raw[t] = *reinterpret_cast<const typename DT::vec4*>(cp);
+      sin_raw[t] = *reinterpret_cast<const typename DT::vec4*>(sp);
+      slot[t] = p.slots64 ? static_cast<const int64_t*>(p.slots)[m]
+                          : static_cast<int64_t>(static_cast<const int32_t*>(p.slots)[m]);
+    }
   }
   if (wave == 0) {
 #pragma unroll
@@ -358,6 +403,52 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 
   // D[4·(lane/16) + r][lane%16] of row tile f: features nf+16f .. +3 of token
   // m.  Each epilogue rounds where the reference's separate tensor ops round.
+  if constexpr (ROPE) {
+    // y = round(acc + bias) is the projection's output (q, k or v of this
+    // head); q and k then rotate as RotaryEmbedding.apply rounds it,
+    //   first half:  round(round(x1*cos) - round(x2*sin)),
+    //   second half: round(round(x2*cos) + round(x1*sin)),
+    // with x1/x2 the dims of the pair in the first/second half, held by this
+    // lane and by lane ^ 32 (same token row, so the exchange happens before
+    // any row check, with every lane of the wave active).
+    const bool second = grp >= 2;
+    const int Hq = p.num_heads, Hkv = p.num_kv_heads, D = p.head_dim;
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int m = m0 + 16 * t + row;
+      float y[4], yp[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        y[r] = from_model<DT>(to_model<DT>(acc[0][t][r] + from_model<DT>(bias_raw[0][r])));
+        yp[r] = __shfl_xor(y[r], 32);
+      }
+      if (m >= p.M) continue;
+      typename DT::vec4 o;
+      if (head < Hq + Hkv) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float c = from_model<DT>(cos_raw[t][r]), sn = from_model<DT>(sin_raw[t][r]);
+          const float a = from_model<DT>(to_model<DT>(y[r] * c));
+          const float b = from_model<DT>(to_model<DT>(yp[r] * sn));
+          o[r] = to_model<DT>(second ? a + b : a - b);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r]);
+      }
+      T* dst;
+      if (head < Hq) {
+        dst = static_cast<T*>(p.out) + (static_cast<int64_t>(m) * Hq + head) * D;
+      } else {
+        if (slot[t] < 0 || slot[t] >= p.num_slots) continue;  // padding / invalid slot: never written
+        const int kvh = head < Hq + Hkv ? head - Hq : head - Hq - Hkv;
+        T* cache = static_cast<T*>(head < Hq + Hkv ? p.k_cache : p.v_cache);
+        dst = cache + (slot[t] * Hkv + kvh) * D;
+      }
+      *reinterpret_cast<typename DT::vec4*>(dst + dim0) = o;
+    }
+    return;
+  }
 #pragma unroll
   for (int f = 0; f < FT; ++f) {
     const int nff = nf + 16 * f;
@@ -413,24 +504,25 @@ struct Shape {
 Shape shape_for(int M, int N, int K, int mt, int mtiles, bool norm) {
   const int chunks = K / 128;
   if (chunks >= 1 && chunks <= 8) {
-    const bool two = !norm && M >= 16 && N % 32 == 0 && static_cast<int64_t>(N / 32) * mtiles >= 256;
+    // (64-token tiles with two feature tiles would spill: 256 VGPRs.)
+    const bool two = !norm && mt == 16 && M >= 16 && N % 32 == 0 && static_cast<int64_t>(N / 32) * mtiles >= 256;
     return {chunks, 1, two ? 2 : 1};
   }
   if (K <= 2048) return {8, 4, 1};
   return {mt <= 16 ? 16 : 8, 4, 1};
 }
 
-template <class DT, int MT, int FT, bool NORM>
+template <class DT, int MT, int FT, bool NORM, bool ROPE = false>
 const void* one_chunk_kernel(int waves) {
   switch (waves) {
-    case 1: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 1, 1, FT, NORM>);
-    case 2: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 2, 1, FT, NORM>);
-    case 3: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 3, 1, FT, NORM>);
-    case 4: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 4, 1, FT, NORM>);
-    case 5: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 5, 1, FT, NORM>);
-    case 6: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 6, 1, FT, NORM>);
-    case 7: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 7, 1, FT, NORM>);
-    default: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 1, FT, NORM>);
+    case 1: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 1, 1, FT, NORM, ROPE>);
+    case 2: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 2, 1, FT, NORM, ROPE>);
+    case 3: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 3, 1, FT, NORM, ROPE>);
+    case 4: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 4, 1, FT, NORM, ROPE>);
+    case 5: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 5, 1, FT, NORM, ROPE>);
+    case 6: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 6, 1, FT, NORM, ROPE>);
+    case 7: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 7, 1, FT, NORM, ROPE>);
+    default: return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 1, FT, NORM, ROPE>);
   }
 }
 
@@ -438,12 +530,29 @@ template <class DT, int MT>
 const void* kernel_for(Shape sh, bool norm) {
   if (sh.batch == 1) {
     if (norm) return one_chunk_kernel<DT, MT, 1, true>(sh.waves);
-    return sh.ft == 2 ? one_chunk_kernel<DT, MT, 2, false>(sh.waves) : one_chunk_kernel<DT, MT, 1, false>(sh.waves);
+    if constexpr (MT == 16) {
+      if (sh.ft == 2) return one_chunk_kernel<DT, MT, 2, false>(sh.waves);
+    }
+    return one_chunk_kernel<DT, MT, 1, false>(sh.waves);
   }
   if constexpr (MT <= 16) {
-    if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4, 1, false>);
+    if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4, 1, false, false>);
   }
-  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 4, 1, false>);
+  return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 8, 4, 1, false, false>);
+}
+
+template <class DT>
+hipError_t launch_int4_linear_rope(const Int4LinearParams& p, hipStream_t stream) {
+  void* args[] = {const_cast<Int4LinearParams*>(&p)};
+  const int mt = p.M <= 64 ? 16 : 64;
+  const int waves = p.K / 128;  // the caller checked 1..8 whole chunks
+  const bool norm = p.norm_weight != nullptr;
+  const void* fn = mt == 16 ? (norm ? one_chunk_kernel<DT, 16, 1, true, true>(waves)
+                                    : one_chunk_kernel<DT, 16, 1, false, true>(waves))
+                            : (norm ? one_chunk_kernel<DT, 64, 1, true, true>(waves)
+                                    : one_chunk_kernel<DT, 64, 1, false, true>(waves));
+  const dim3 grid(static_cast<unsigned>(p.N / 16), static_cast<unsigned>((p.M + mt - 1) / mt));
+  return hipLaunchKernel(fn, grid, dim3(64 * waves), args, 0, stream);
 }
 
 template <class DT>
@@ -507,7 +616,7 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
       !aligned(qweight, 16) || !aligned(scales, 4) || (bias && !aligned(bias, 2)))
     return NS_ERR_INVALID_ARG;
 
-  Int4LinearParams p;
+  Int4LinearParams p{};
   p.out = out;
   p.x = static_cast<const char*>(x);
   p.x_stride = x_stride_row;
@@ -526,6 +635,70 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   p.groups = K / group_size;
   const hipStream_t s = static_cast<hipStream_t>(stream);
   const hipError_t e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s) : launch_int4_linear<BF16>(p, s);
+  return e == hipSuccess ? NS_OK : NS_ERR_HIP;
+}
+
+extern "C" int ns_int4_linear_rope_cache(void* q_out, const void* x, int64_t x_stride_row,
+                                         const void* qweight, const void* scales, const void* zeros,
+                                         const void* bias, const void* norm_weight, float norm_eps,
+                                         const void* cos, const void* sin, int64_t cos_sin_stride_token,
+                                         void* k_cache, void* v_cache,
+                                         const void* slot_mapping, int slot_mapping_is_int64,
+                                         int64_t M, int K, int group_size,
+                                         int num_heads, int num_kv_heads, int head_dim,
+                                         int block_size, int64_t num_blocks, int dtype, void* stream) {
+  using namespace ns;
+  if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
+  if (M < 0 || K <= 0 || group_size <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 ||
+      block_size <= 0 || num_blocks < 0)
+    return NS_ERR_INVALID_ARG;
+  // 16-row tiles pair dims of the two halves of a head; one 128-wide chunk per wave.
+  if (head_dim % 16 != 0 || K % 128 != 0 || K / 128 > 8 || group_size % 32 != 0 || K % group_size != 0)
+    return NS_ERR_UNSUPPORTED;
+  if (M == 0) return NS_OK;
+  if (!q_out || !x || !qweight || !scales || !zeros || !cos || !sin || !k_cache || !v_cache || !slot_mapping)
+    return NS_ERR_INVALID_ARG;
+  if ((M + 15) / 16 > 65535) return NS_ERR_INVALID_ARG;
+  const int64_t n_rows = static_cast<int64_t>(num_heads + 2 * num_kv_heads) * head_dim;
+  if (n_rows / 16 > 0x7FFFFFFF) return NS_ERR_INVALID_ARG;
+  if (x_stride_row < K || x_stride_row % 8 != 0 || !aligned(x, 16) || !aligned(qweight, 16) ||
+      !aligned(scales, 4) || (bias && !aligned(bias, 2)) || (norm_weight && !aligned(norm_weight, 16)) ||
+      !aligned(q_out, 8) || !aligned(k_cache, 8) || !aligned(v_cache, 8) || !aligned(cos, 8) ||
+      !aligned(sin, 8) || cos_sin_stride_token < head_dim || cos_sin_stride_token % 4 != 0 ||
+      !aligned(slot_mapping, slot_mapping_is_int64 ? 8 : 4))
+    return NS_ERR_INVALID_ARG;
+
+  Int4LinearParams p{};
+  p.out = q_out;
+  p.x = static_cast<const char*>(x);
+  p.x_stride = x_stride_row;
+  p.qweight = static_cast<const uint8_t*>(qweight);
+  p.scales = static_cast<const float*>(scales);
+  p.zeros = static_cast<const uint8_t*>(zeros);
+  p.bias = bias;
+  p.residual = nullptr;
+  p.norm_weight = norm_weight;
+  p.norm_eps = norm_eps;
+  p.epilogue = NS_EPILOGUE_NONE;
+  p.M = static_cast<int>(M);
+  p.N = static_cast<int>(n_rows);
+  p.K = K;
+  p.group_size = group_size;
+  p.groups = K / group_size;
+  p.cos = cos;
+  p.sin = sin;
+  p.cs_stride = cos_sin_stride_token;
+  p.k_cache = k_cache;
+  p.v_cache = v_cache;
+  p.slots = slot_mapping;
+  p.slots64 = slot_mapping_is_int64 ? 1 : 0;
+  p.num_slots = num_blocks * static_cast<int64_t>(block_size);
+  p.num_heads = num_heads;
+  p.num_kv_heads = num_kv_heads;
+  p.head_dim = head_dim;
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const hipError_t e =
+      dtype == NS_DTYPE_F16 ? launch_int4_linear_rope<F16>(p, s) : launch_int4_linear_rope<BF16>(p, s);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }
 

@@ -24,7 +24,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .quant import Int4Linear
+from .quant import Int4Linear, int4_qkv_rope_cache
 from .rotary import RotaryEmbedding, rope_reshape_and_cache
 
 
@@ -109,7 +109,12 @@ class Qwen2Attention(nn.Module):
         self.qkv_proj: nn.Module | None = None
 
     def fuse(self) -> None:
-        self.qkv_proj = _concat_linears([self.q_proj, self.k_proj, self.v_proj])
+        qkv = _concat_linears([self.q_proj, self.k_proj, self.v_proj])
+        if isinstance(qkv, Int4Linear) and self.head_dim % 16 == 0:
+            # Rows in rotary-pair order: rotary and the cache write run in the
+            # projection's epilogue (ns_int4_linear_rope_cache).
+            qkv = Int4Linear.rope_pairs(qkv, self.num_heads, self.num_kv_heads, self.head_dim)
+        self.qkv_proj = qkv
         del self.q_proj, self.k_proj, self.v_proj
 
     def forward(self, hidden, cos, sin, kv_cache, md, attn_fn, residual=None, norm=None):
@@ -119,6 +124,11 @@ class Qwen2Attention(nn.Module):
         Hq, Hkv, D = self.num_heads, self.num_kv_heads, self.head_dim
         if norm is not None and not (isinstance(self.qkv_proj, Int4Linear) and self.qkv_proj.fuses_norm):
             hidden, norm = norm(hidden), None
+        kc, vc = kv_cache.k_cache[self.layer_idx], kv_cache.v_cache[self.layer_idx]
+        if isinstance(self.qkv_proj, Int4Linear) and self.qkv_proj.rope_heads is not None:
+            q = int4_qkv_rope_cache(hidden, self.qkv_proj, cos, sin, kc, vc, md.slot_mapping, norm=norm)
+            out = attn_fn(q, kc, vc, md, self.scale)
+            return _linear(self.o_proj, out.view(T, Hq * D), residual)
         if self.qkv_proj is not None:
             qkv = self.qkv_proj(hidden, norm=norm) if norm is not None else self.qkv_proj(hidden)
             q = qkv[:, :Hq * D].view(T, Hq, D)
@@ -130,7 +140,6 @@ class Qwen2Attention(nn.Module):
             v = self.v_proj(hidden).view(T, Hkv, D)
         # Rotary on q and k, then k and v into the cache before attention reads
         # it (a prefill chunk attends to the keys it just produced).
-        kc, vc = kv_cache.k_cache[self.layer_idx], kv_cache.v_cache[self.layer_idx]
         q = rope_reshape_and_cache(q, k, v, cos, sin, kc, vc, md.slot_mapping)
         out = attn_fn(q, kc, vc, md, self.scale)
         return _linear(self.o_proj, out.view(T, Hq * D), residual)

@@ -166,6 +166,67 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
     return out.view(*lead, n_out)
 
 
+def rope_pair_order(num_heads: int, head_dim: int) -> torch.Tensor:
+    """Row order of a q|k|v weight for ns_int4_linear_rope_cache: new row r is original row order[r].
+
+    Each head's rows are regrouped in 16-row tiles; tile i holds dims
+    [8i, 8i+8) then [D/2 + 8i, D/2 + 8i + 8), so the MFMA result puts every
+    dim and its rotate_half partner in lanes 32 apart."""
+    D = head_dim
+    if D % 16 != 0:
+        raise ValueError(f"head_dim must be a multiple of 16, got {D}")
+    j = torch.arange(16)
+    tiles = torch.stack([torch.where(j < 8, 8 * i + j, D // 2 + 8 * i + (j - 8)) for i in range(D // 16)])
+    per_head = tiles.reshape(-1)
+    return (torch.arange(num_heads).unsqueeze(1) * D + per_head).reshape(-1)
+
+
+def int4_qkv_rope_cache(x: torch.Tensor, qkv: "Int4Linear", cos: torch.Tensor, sin: torch.Tensor,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                        norm=None) -> torch.Tensor:
+    """q' for attention, with k' and v written to the cache: one ns_int4_linear_rope_cache launch.
+
+    qkv is a rope-paired q|k|v module (Int4Linear.rope_pairs); x [T, K];
+    cos/sin [T, 1, D] or [T, D] in x's dtype; norm an RMSNorm-like module run
+    in the same launch.  Above FUSED_MAX_ROWS tokens (prefill chunks) this is
+    the dequantised-weight projection followed by ns_rope_reshape_and_cache.
+    Returns q' as a contiguous [T, Hq, D] tensor."""
+    from .rotary import rope_reshape_and_cache
+
+    Hq, Hkv, D = qkv.rope_heads
+    T, K = x.shape
+    if T > FUSED_MAX_ROWS or not qkv.fuses_norm:
+        y = qkv(x, norm=norm)
+        q, k, v = y[:, :Hq * D].view(T, Hq, D), y[:, Hq * D:(Hq + Hkv) * D].view(T, Hkv, D), y[:, (Hq + Hkv) * D:].view(T, Hkv, D)
+        return rope_reshape_and_cache(q, k, v, cos, sin, k_cache, v_cache, slot_mapping)
+    lib = _lib.load()
+    cs, sn = cos.reshape(T, D), sin.reshape(T, D)
+    if not (x.dtype == cos.dtype == sin.dtype == k_cache.dtype == v_cache.dtype):
+        raise TypeError("x, cos, sin and the caches must share one dtype")
+    if cs.stride(1) != 1 or sn.stride(0) != cs.stride(0) or sn.stride(1) != 1:
+        raise ValueError("cos and sin must be [T, D] rows with one token stride")
+    if k_cache.dim() != 4 or v_cache.shape != k_cache.shape or k_cache.shape[2:] != (Hkv, D):
+        raise ValueError(f"caches must be [num_blocks, block_size, {Hkv}, {D}]")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("caches must be contiguous")
+    if slot_mapping.shape != (T,) or slot_mapping.dtype not in (torch.int32, torch.int64):
+        raise ValueError(f"slot_mapping must be a [{T}] int32/int64 tensor")
+    x2 = x if (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) else x.contiguous()
+    slots = slot_mapping if slot_mapping.is_contiguous() else slot_mapping.contiguous()
+    out = torch.empty((T, Hq, D), dtype=x.dtype, device=x.device)
+    rc = lib.ns_int4_linear_rope_cache(
+        out.data_ptr(), x2.data_ptr(), x2.stride(0),
+        qkv.qweight.data_ptr(), qkv.scales.data_ptr(), qkv.zeros.data_ptr(),
+        None if qkv.bias is None else qkv.bias.data.data_ptr(),
+        None if norm is None else norm.weight.data.data_ptr(), 1e-6 if norm is None else float(norm.variance_epsilon),
+        cs.data_ptr(), sn.data_ptr(), cs.stride(0),
+        k_cache.data_ptr(), v_cache.data_ptr(), slots.data_ptr(), int(slots.dtype == torch.int64),
+        T, K, qkv.group_size, Hq, Hkv, D, k_cache.shape[1], k_cache.shape[0],
+        _lib.DTYPE_CODES[x.dtype], torch.cuda.current_stream(x.device).cuda_stream)
+    _lib.check(rc, "ns_int4_linear_rope_cache")
+    return out
+
+
 class Int4Linear(nn.Module):
     """Drop-in nn.Linear whose weight lives as INT4 groups (reference QuantLinear, int4 mode).
 
@@ -189,6 +250,10 @@ class Int4Linear(nn.Module):
         self.bias = nn.Parameter(torch.zeros(out_features, dtype=dtype, device=device)) if bias else None
         # Rows interleaved as (gate, up) pairs whose output is silu(gate) * up.
         self.silu_mul = False
+        # (num_heads, num_kv_heads, head_dim) when the rows are q|k|v in
+        # rotary-pair order (rope_pairs); forward() then restores row order.
+        self.rope_heads: tuple[int, int, int] | None = None
+        self.rope_inverse: torch.Tensor | None = None
 
     @classmethod
     def from_linear(cls, lin: nn.Linear, group_size: int = 128) -> "Int4Linear":
@@ -207,11 +272,14 @@ class Int4Linear(nn.Module):
         variance_epsilon) applied inside the launch when the shape allows."""
         if norm is not None and not self.fuses_norm:
             x, norm = norm(x), None
-        return int4_linear(x, self.qweight, self.scales, self.zeros,
-                           None if self.bias is None else self.bias.data, self.group_size,
-                           residual=residual, silu_mul=self.silu_mul,
-                           norm_weight=None if norm is None else norm.weight.data,
-                           norm_eps=1e-6 if norm is None else norm.variance_epsilon)
+        if self.rope_heads is not None and residual is not None:
+            raise ValueError("a rope-paired q|k|v projection takes no residual")
+        y = int4_linear(x, self.qweight, self.scales, self.zeros,
+                        None if self.bias is None else self.bias.data, self.group_size,
+                        residual=residual, silu_mul=self.silu_mul,
+                        norm_weight=None if norm is None else norm.weight.data,
+                        norm_eps=1e-6 if norm is None else norm.variance_epsilon)
+        return y if self.rope_inverse is None else y.index_select(-1, self.rope_inverse)
 
     @property
     def fuses_norm(self) -> bool:
@@ -234,6 +302,24 @@ class Int4Linear(nn.Module):
             a, b = getattr(gate, name), getattr(up, name)
             getattr(m, name).copy_(torch.stack([a, b], dim=1).reshape(-1, a.shape[1]))
         m.silu_mul = True
+        return m
+
+    @classmethod
+    def rope_pairs(cls, qkv: "Int4Linear", num_heads: int, num_kv_heads: int, head_dim: int) -> "Int4Linear":
+        """The q|k|v module with its rows in rotary-pair order (rope_pair_order),
+        for int4_qkv_rope_cache; calling it still returns rows in q|k|v order."""
+        heads = num_heads + 2 * num_kv_heads
+        if qkv.out_features != heads * head_dim or qkv.silu_mul:
+            raise ValueError("rope_pairs needs a q|k|v projection of (Hq + 2 Hkv) * D rows")
+        order = rope_pair_order(heads, head_dim).to(qkv.qweight.device)
+        m = cls(qkv.in_features, qkv.out_features, qkv.bias is not None, qkv.group_size, qkv.compute_dtype,
+                qkv.qweight.device)
+        for name in ("qweight", "scales", "zeros"):
+            getattr(m, name).copy_(getattr(qkv, name).index_select(0, order))
+        if qkv.bias is not None:
+            m.bias.data.copy_(qkv.bias.data.index_select(0, order))
+        m.rope_heads = (num_heads, num_kv_heads, head_dim)
+        m.rope_inverse = torch.argsort(order)
         return m
 
     def extra_repr(self) -> str:

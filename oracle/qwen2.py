@@ -34,6 +34,28 @@ def _weight(module, dtype_name: str) -> tuple[torch.Tensor, torch.Tensor | None]
     return w, b
 
 
+def _rope_pair_order_ref(heads: int, D: int) -> list[int]:
+    """Stored row r of a rope-paired q|k|v weight holds original row order[r]:
+    16-row tile i of each head holds dims [8i, 8i+8) then [D/2 + 8i, D/2 + 8i + 8)
+    (the layout ns_int4_linear_rope_cache documents; restated here, not imported)."""
+    return [h * D + (8 * i + j if j < 8 else D // 2 + 8 * i + (j - 8))
+            for h in range(heads) for i in range(D // 16) for j in range(16)]
+
+
+def _qkv_weight(module, dtype_name: str):
+    """(W, b) of a fused q|k|v module in q|k|v row order."""
+    w, b = _weight(module, dtype_name)
+    heads = getattr(module, "rope_heads", None)
+    if heads is not None:
+        Hq, Hkv, D = heads
+        order = torch.tensor(_rope_pair_order_ref(Hq + 2 * Hkv, D))
+        inv = torch.empty_like(order)
+        inv[order] = torch.arange(order.numel())
+        w = w[inv]
+        b = None if b is None else b[inv]
+    return w, b
+
+
 def _rms(x, w, eps):
     return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
 
@@ -63,7 +85,7 @@ def qwen2_forward_ref(model, input_ids, positions, k_caches, v_caches, md, sampl
         att, mlp = layer.self_attn, layer.mlp
         x = _rms(h, layer.input_layernorm.weight.detach().cpu().float(), cfg.rms_norm_eps)
         if att.qkv_proj is not None:
-            w, b = _weight(att.qkv_proj, name)
+            w, b = _qkv_weight(att.qkv_proj, name)
             qkv = x @ w.T + b
             q, k, v = qkv[:, :Hq * D], qkv[:, Hq * D:(Hq + Hkv) * D], qkv[:, (Hq + Hkv) * D:]
         else:

@@ -300,3 +300,57 @@ def test_a_row_does_not_depend_on_the_rest_of_the_batch(dtype, K):
             wq = dequantize_int4_ref(packed.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(), gs, NAME[dtype])
             _check(many, int4_linear_ref(x.float().cpu().numpy(), wq, b.float().cpu().numpy()), dtype,
                    f"M=64 N={N} K={K}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 7, 32, 64, 100, 200])
+@pytest.mark.parametrize("heads", [(14, 2, 64), (4, 2, 128)], ids=["qwen0.5b", "d128"])
+@pytest.mark.parametrize("with_norm", [True, False], ids=["norm", "no_norm"])
+def test_rope_cache_epilogue_matches_projection_then_rotary(dtype, M, heads, with_norm):
+    """ns_int4_linear_rope_cache == q|k|v projection, then ns_rope_reshape_and_cache, bit for bit.
+
+    Checks q', the rotated keys and the values in both caches, with padding
+    slots (-1) that must stay untouched, int32 and int64 slot mappings, and
+    the >128-token fallback through the dequantised weight."""
+    from nanoserve_amd.model import RMSNorm
+    from nanoserve_amd.quant import Int4Linear, int4_qkv_rope_cache
+    from nanoserve_amd.rotary import RotaryEmbedding, rope_reshape_and_cache
+
+    Hq, Hkv, D = heads
+    K = 896 if D == 64 else 512
+    N = (Hq + 2 * Hkv) * D
+    g = torch.Generator().manual_seed(61 + M)
+    lin = torch.nn.Linear(K, N, bias=True).to(dtype)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(N, K, generator=g) * 0.05)
+        lin.bias.copy_(torch.randn(N, generator=g) * 0.1)
+    plain = Int4Linear.from_linear(lin, 128).to(DEV)
+    paired = Int4Linear.rope_pairs(plain, Hq, Hkv, D)
+    norm = None
+    if with_norm:
+        norm = RMSNorm(K, eps=1e-6).to(dtype).to(DEV)
+        with torch.no_grad():
+            norm.weight.copy_((1 + 0.1 * torch.randn(K, generator=g)).to(dtype))
+    x = (torch.randn(M, K, generator=g) * 2).to(dtype).to(DEV)
+    rot = RotaryEmbedding(D, 4096, base=1e6, device=DEV)
+    pos = torch.randint(0, 4096, (M,), generator=g).to(DEV)
+    cos, sin = rot.cos_sin(pos, dtype)
+    nb, bs = 64, 16
+    slots = torch.randperm(nb * bs, generator=g)[:M]
+    slots[::5] = -1
+    kc0 = torch.randn(nb, bs, Hkv, D, generator=g).to(dtype).to(DEV)
+    vc0 = torch.randn(nb, bs, Hkv, D, generator=g).to(dtype).to(DEV)
+    for slot_dtype in (torch.int32, torch.int64):
+        sm = slots.to(slot_dtype).to(DEV)
+        y = plain(x, norm=norm)
+        q, k, v = y[:, :Hq * D].view(M, Hq, D), y[:, Hq * D:(Hq + Hkv) * D].view(M, Hkv, D), y[:, (Hq + Hkv) * D:].view(M, Hkv, D)
+        kc_a, vc_a = kc0.clone(), vc0.clone()
+        q_a = rope_reshape_and_cache(q, k, v, cos, sin, kc_a, vc_a, sm)
+        kc_b, vc_b = kc0.clone(), vc0.clone()
+        q_b = int4_qkv_rope_cache(x, paired, cos, sin, kc_b, vc_b, sm, norm=norm)
+        torch.cuda.synchronize()
+        assert torch.equal(q_a, q_b), f"q' differs: {(q_a.float() - q_b.float()).abs().max().item():.3e}"
+        assert torch.equal(kc_a, kc_b), "key cache differs"
+        assert torch.equal(vc_a, vc_b), "value cache differs"
+        # The module still returns rows in q|k|v order.
+        assert torch.equal(paired(x, norm=norm), y)

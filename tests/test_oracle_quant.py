@@ -109,3 +109,23 @@ def test_product_quantizer_equals_oracle(shape, gs):
     assert np.array_equal(packed.numpy(), rp)
     assert np.array_equal(s.numpy(), rs)
     assert np.array_equal(z.numpy(), rz)
+
+
+@pytest.mark.parametrize("heads,D", [(18, 64), (8, 128), (1, 16)])
+def test_rope_pair_row_order(heads, D):
+    """The stored order of a rope-paired q|k|v weight: a permutation of each head's
+    rows in which row r and row r + 8 of every 16-row tile are a rotate_half pair
+    (dims d and d + D/2), lane groups g and g ^ 2 of the MFMA result; the
+    product's order (nanoserve_amd.quant.rope_pair_order) is the oracle's."""
+    from oracle.qwen2 import _rope_pair_order_ref
+    from nanoserve_amd.quant import rope_pair_order
+
+    order = _rope_pair_order_ref(heads, D)
+    assert sorted(order) == list(range(heads * D))
+    for t in range(0, heads * D, 16):
+        tile = order[t:t + 16]
+        head = tile[0] // D
+        assert all(o // D == head for o in tile)
+        for r in range(8):
+            assert tile[r + 8] - tile[r] == D // 2 and tile[r] % D < D // 2
+    assert rope_pair_order(heads, D).tolist() == order
