@@ -13,7 +13,11 @@ Linear layers are nn.Linear or, after `quantize_model`, Int4Linear
 (ns_int4_linear).  `fuse_projections()` concatenates q/k/v into one
 projection and gate/up into another (row concatenation, so INT4 groups are
 unchanged), which turns 5 GEMM launches per layer into 2; q, k and v are then
-column views of the fused output, which the rotary kernel reads in place.
+column views of the fused output, which the rotary kernel reads in place.  A
+fused INT4 q|k|v projection keeps each head's rows in rotary-pair order and
+runs rotary and the cache write in its own epilogue
+(ns_int4_linear_rope_cache), so projection, rotary and cache write are one
+launch.
 """
 
 from __future__ import annotations
