@@ -153,6 +153,28 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                    int64_t M, int N, int K, int group_size, int dtype, void* stream);
 
 /*
+ * ns_int4_linear_splitk -- ns_int4_linear with the K loop of long-K layers
+ * split over several workgroups per 16-feature tile (down_proj of
+ * Qwen2.5-0.5B: N = 896 is 56 tiles, too few for the device, each walking
+ * K = 4864).  Same operands, epilogues and prologue as ns_int4_linear; the
+ * fp32 partial sums of each split go to `workspace` and the last split of a
+ * tile adds them in split order (deterministic) and runs the epilogue.  The
+ * split count (up to 4) keeps tiles x splits within 256 workgroups, so it
+ * depends on N, K and the number of token tiles.  Same replacement as ns_int4_linear (reference
+ * nanoserve/quant.py:157-158).  workspace: 256-byte aligned,
+ * ns_int4_linear_splitk_workspace_size(M, N, K) bytes, zeroed once before
+ * first use; every call leaves its arrival counters at zero.  Calls that
+ * overlap in time must not share a workspace.  Shapes that do not split
+ * (size 0) ignore it.
+ */
+size_t ns_int4_linear_splitk_workspace_size(int64_t M, int N, int K);
+int ns_int4_linear_splitk(void* out, const void* x, int64_t x_stride_row,
+                          const void* qweight, const void* scales, const void* zeros, const void* bias,
+                          const void* residual, int epilogue, const void* norm_weight, float norm_eps,
+                          int64_t M, int N, int K, int group_size, int dtype,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * ns_int4_linear_rope_cache -- the q|k|v projection of one attention layer
  * with the rotary embedding and the paged-cache write in its epilogue: one
  * launch for what the reference runs as QuantLinear.forward of q, k and v

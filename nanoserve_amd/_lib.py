@@ -70,6 +70,16 @@ SIGNATURES = {
         c_int64, c_int, c_int, c_int,            # M, N, K, group_size
         c_int, c_void_p,                         # dtype, stream
     ]),
+    "ns_int4_linear_splitk_workspace_size": (c_size_t, [c_int64, c_int, c_int]),  # M, N, K
+    "ns_int4_linear_splitk": (c_int, [
+        c_void_p, c_void_p, c_int64,             # out, x, x row stride
+        c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)
+        c_void_p, c_int,                         # residual (or None), epilogue
+        c_void_p, c_float,                       # RMSNorm weight (or None), eps
+        c_int64, c_int, c_int, c_int,            # M, N, K, group_size
+        c_int,                                   # dtype
+        c_void_p, c_size_t, c_void_p,            # workspace, bytes, stream
+    ]),
     "ns_int4_linear_rope_cache": (c_int, [
         c_void_p, c_void_p, c_int64,             # q_out, x, x row stride
         c_void_p, c_void_p, c_void_p, c_void_p,  # qweight, scales, zeros, bias (or None)

@@ -57,7 +57,21 @@ struct Int4LinearParams {
   int slots64;
   int64_t num_slots;
   int num_heads, num_kv_heads, head_dim;
+  // Split-K (multi-chunk kernels, gridDim.z = splits > 1): partial sums of
+  // every (tile, split) go to `part`, arrivals are counted in `counters` (one
+  // per tile, zero between calls) and the last split of a tile finishes it.
+  float* part;
+  unsigned* counters;
+  int part_bytes;
 };
+
+// Device-scope (sc1) buffer accesses carry partials between workgroups, which
+// may sit on different XCDs whose L2s are not coherent with each other: the
+// stores write through to the device coherence point and the loads bypass the
+// non-coherent caches, so a split's stores only need to be acknowledged
+// (s_waitcnt vmcnt(0)) before its arrival is counted.
+constexpr int kSc1 = 16;                  // cache-policy bit SC1 of gfx950 buffer ops
+constexpr int kBufferWord3 = 0x00020000;  // raw 32-bit buffer descriptor, word 3
 
 // Row order of a q|k|v weight for the rotary epilogue.  Within each head of
 // D rows, 16-row tile i holds dims [8i, 8i+8) then [D/2+8i, D/2+8i+8): lane
@@ -283,8 +297,12 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   // needed 74 VGPRs instead of 52 (two feature tiles: 128 instead of 77).
   const bool normed = NORM || p.norm_weight != nullptr;
   const int chunks = normed ? 0 : p.K / 128;
-  const int c_beg = (chunks * wave) / WAVES;
-  const int c_end = (chunks * (wave + 1)) / WAVES;
+  // Split z of gridDim.z takes chunks [chunks·z/S, chunks·(z+1)/S) (S = 1
+  // unless the host asked for split-K); its waves divide them.
+  const int S = static_cast<int>(gridDim.z), z = static_cast<int>(blockIdx.z);
+  const int cz0 = (chunks * z) / S, czn = (chunks * (z + 1)) / S - cz0;
+  const int c_beg = cz0 + (czn * wave) / WAVES;
+  const int c_end = cz0 + (czn * (wave + 1)) / WAVES;
   if constexpr (BATCH == 1) {
     // One chunk per wave (K up to 8 chunks): the chunk's codes, scale, zero
     // point and x operands are all issued before any of them is used, so the
@@ -366,7 +384,7 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
   }
   // Remaining 32-wide steps when K is not a multiple of 128.
-  for (int s = normed ? p.K / 32 : 4 * chunks + wave; s < p.K / 32; s += WAVES) {
+  for (int s = normed || z != S - 1 ? p.K / 32 : 4 * chunks + wave; s < p.K / 32; s += WAVES) {
     const int k = 32 * s + 8 * grp;
     const int gi = k / p.group_size;
     V8 b[NT];
@@ -399,6 +417,40 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 #pragma unroll
         for (int w = 0; w < WAVES - 1; ++w) acc[f][t] += red[w][f][t][lane];
       }
+  }
+
+  if constexpr (BATCH > 1) {
+    if (S > 1) {
+      // Publish this split's sums, count the arrival; the last split of the
+      // tile adds all S partials in split order (its own included, so the
+      // result does not depend on which split came last) and resets the counter.
+      const int tile = static_cast<int>(blockIdx.y * gridDim.x + blockIdx.x);
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(p.part, static_cast<short>(0), p.part_bytes, kBufferWord3);
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[0][t]), rs,
+                                               (((tile * S + z) * NT + t) * 64 + lane) * 16, 0, kSc1);
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are acknowledged
+      unsigned prev = 0;
+      if (lane == 0) prev = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __shfl(prev, 0);
+      if (prev != static_cast<unsigned>(S - 1)) return;
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        floatx4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int zz = 0; zz < S; ++zz) {
+          const int off = (((tile * S + zz) * NT + t) * 64 + lane) * 16;
+          floatx4 v;
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            v[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rs, off + 4 * r, 0, kSc1));
+          sum += v;
+        }
+        acc[0][t] = sum;
+      }
+      if (lane == 0) __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 
   // D[4·(lane/16) + r][lane%16] of row tile f: features nf+16f .. +3 of token
@@ -555,8 +607,23 @@ hipError_t launch_int4_linear_rope(const Int4LinearParams& p, hipStream_t stream
   return hipLaunchKernel(fn, grid, dim3(64 * waves), args, 0, stream);
 }
 
+// Split-K for the multi-chunk kernels: few workgroups (down_proj: N = 896 is
+// 56 tiles of 16 features per token tile) each walking 38 chunks leave most
+// CUs idle, so each tile's chunks are split over up to 4 workgroups while the
+// grid stays within one workgroup per CU (a 16-wave workgroup fills one).
+// Measured on MI355X for down_proj + residual, graph-replayed: 8 / 16 tokens
+// 7.16 / 8.50 -> 6.62 / 6.99 us with 4 splits; 4 splits at 32 and 64 tokens
+// (448 and 896 workgroups, two dispatch rounds) were slower, 8.61 / 8.88 ->
+// 9.24 / 12.42 us.
+int splitk_for(int N, int K, int64_t mtiles) {
+  const int chunks = K / 128;
+  if (chunks <= 8 || K <= 2048) return 1;
+  const int64_t tiles = static_cast<int64_t>(N / 16) * mtiles;
+  return 4 * tiles <= 256 ? 4 : 2 * tiles <= 256 ? 2 : 1;
+}
+
 template <class DT>
-hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
+hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream, int splits = 1) {
   void* args[] = {const_cast<Int4LinearParams*>(&p)};
   // Up to 64 tokens, 16-token tiles (grid.y tiles side by side) beat wider
   // ones: more waves in flight and fewer registers each (measured on MI355X,
@@ -567,7 +634,8 @@ hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream) {
   const bool norm = p.norm_weight != nullptr;
   const Shape sh = shape_for(p.M, p.N, p.K, mt, mtiles, norm);
   const void* fn = mt == 16 ? kernel_for<DT, 16>(sh, norm) : kernel_for<DT, 64>(sh, norm);
-  const dim3 grid(static_cast<unsigned>(p.N / (16 * sh.ft)), static_cast<unsigned>(mtiles));
+  const dim3 grid(static_cast<unsigned>(p.N / (16 * sh.ft)), static_cast<unsigned>(mtiles),
+                  static_cast<unsigned>(sh.batch > 1 ? splits : 1));
   return hipLaunchKernel(fn, grid, dim3(64 * sh.waves), args, 0, stream);
 }
 
@@ -594,11 +662,30 @@ __global__ __launch_bounds__(256) void int4_dequantize_kernel(typename DT::T* ou
 }  // namespace
 }  // namespace ns
 
-extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
-                              const void* qweight, const void* scales, const void* zeros, const void* bias,
-                              const void* residual, int epilogue, const void* norm_weight, float norm_eps,
-                              int64_t M, int N, int K, int group_size, int dtype, void* stream) {
-  using namespace ns;
+namespace ns {
+namespace {
+
+// Split-K workspace: one u32 arrival counter per tile (zero between calls),
+// padded to 256 bytes, then the partial sums, 16 bytes per lane, tile and split.
+struct SplitkLayout {
+  int splits;
+  int64_t counter_bytes, part_bytes;
+};
+
+SplitkLayout splitk_layout(int64_t M, int N, int K) {
+  const int mt = M <= 64 ? 16 : 64;
+  const int64_t tiles = static_cast<int64_t>(N / 16) * ((M + mt - 1) / mt);
+  SplitkLayout l;
+  l.splits = M > 0 ? splitk_for(N, K, (M + mt - 1) / mt) : 1;
+  l.counter_bytes = l.splits > 1 ? (tiles * 4 + 255) / 256 * 256 : 0;
+  l.part_bytes = l.splits > 1 ? tiles * l.splits * (mt / 16) * 64 * 16 : 0;
+  return l;
+}
+
+int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void* qweight, const void* scales,
+                      const void* zeros, const void* bias, const void* residual, int epilogue,
+                      const void* norm_weight, float norm_eps, int64_t M, int N, int K, int group_size, int dtype,
+                      void* stream, void* workspace, size_t workspace_bytes, bool splitk) {
   if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
   if (M < 0 || N <= 0 || K <= 0 || group_size <= 0) return NS_ERR_INVALID_ARG;
   if (epilogue != NS_EPILOGUE_NONE && epilogue != NS_EPILOGUE_RESIDUAL && epilogue != NS_EPILOGUE_SILU_MUL)
@@ -633,9 +720,49 @@ extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
   p.K = K;
   p.group_size = group_size;
   p.groups = K / group_size;
+  int splits = 1;
+  if (splitk) {
+    const SplitkLayout l = splitk_layout(M, N, K);
+    if (l.splits > 1) {
+      if (!workspace || !aligned(workspace, 256) ||
+          workspace_bytes < static_cast<size_t>(l.counter_bytes + l.part_bytes) || l.part_bytes > 0x7FFFFFFF)
+        return NS_ERR_INVALID_ARG;
+      p.counters = static_cast<unsigned*>(workspace);
+      p.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + l.counter_bytes);
+      p.part_bytes = static_cast<int>(l.part_bytes);
+      splits = l.splits;
+    }
+  }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s) : launch_int4_linear<BF16>(p, s);
+  const hipError_t e =
+      dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s, splits) : launch_int4_linear<BF16>(p, s, splits);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
+}
+
+}  // namespace
+}  // namespace ns
+
+extern "C" int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
+                              const void* qweight, const void* scales, const void* zeros, const void* bias,
+                              const void* residual, int epilogue, const void* norm_weight, float norm_eps,
+                              int64_t M, int N, int K, int group_size, int dtype, void* stream) {
+  return ns::int4_linear_entry(out, x, x_stride_row, qweight, scales, zeros, bias, residual, epilogue, norm_weight,
+                               norm_eps, M, N, K, group_size, dtype, stream, nullptr, 0, false);
+}
+
+extern "C" size_t ns_int4_linear_splitk_workspace_size(int64_t M, int N, int K) {
+  if (M < 0 || N <= 0 || K <= 0) return 0;
+  const ns::SplitkLayout l = ns::splitk_layout(M, N, K);
+  return static_cast<size_t>(l.counter_bytes + l.part_bytes);
+}
+
+extern "C" int ns_int4_linear_splitk(void* out, const void* x, int64_t x_stride_row,
+                                     const void* qweight, const void* scales, const void* zeros, const void* bias,
+                                     const void* residual, int epilogue, const void* norm_weight, float norm_eps,
+                                     int64_t M, int N, int K, int group_size, int dtype,
+                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return ns::int4_linear_entry(out, x, x_stride_row, qweight, scales, zeros, bias, residual, epilogue, norm_weight,
+                               norm_eps, M, N, K, group_size, dtype, stream, workspace, workspace_bytes, true);
 }
 
 extern "C" int ns_int4_linear_rope_cache(void* q_out, const void* x, int64_t x_stride_row,

@@ -85,16 +85,25 @@ def quantize_int4_groupwise(w: torch.Tensor, group_size: int = 128):
 
 
 @torch.inference_mode()
+def splitk_workspace_bytes(N: int, K: int) -> int:
+    """Workspace bytes that cover every fused-path token count (1..FUSED_MAX_ROWS) of an N x K layer."""
+    lib = _lib.load()
+    return max(int(lib.ns_int4_linear_splitk_workspace_size(m, N, K)) for m in range(1, FUSED_MAX_ROWS + 1))
+
+
 def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
                 bias: torch.Tensor | None, group_size: int, out: torch.Tensor | None = None,
                 residual: torch.Tensor | None = None, silu_mul: bool = False,
                 norm_weight: torch.Tensor | None = None, norm_eps: float = 1e-6,
-                method: str = "auto") -> torch.Tensor:
+                method: str = "auto", workspace: torch.Tensor | None = None) -> torch.Tensor:
     """x [..., K] -> [..., N] through ns_int4_linear (HIP; no CPU fallback).
 
     norm_weight: RMS-normalise the rows of x with this [K] weight inside the
     same launch first (the reference's RMSNorm before the projection; K must
     be a multiple of 128 and at most 1024).
+    workspace: a zeroed uint8 buffer of splitk_workspace_bytes(N, K) bytes;
+    given, long-K layers split their K loop over several workgroups per tile
+    (ns_int4_linear_splitk).  Calls that overlap in time must not share one.
     method: "fused" (ns_int4_linear), "dequant" (ns_int4_dequantize, then a
     library GEMM and the same epilogue as tensor ops) or "auto" (fused up to
     FUSED_MAX_ROWS rows).
@@ -156,12 +165,22 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
         if norm_weight.shape != (K,) or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous():
             raise ValueError(f"norm_weight must be a contiguous [{K}] {x.dtype} tensor")
         nw_ptr = norm_weight.data_ptr()
+    stream = torch.cuda.current_stream(x.device).cuda_stream
+    if workspace is not None:
+        if workspace.dtype != torch.uint8 or not workspace.is_cuda or workspace.data_ptr() % 256 != 0:
+            raise ValueError("workspace must be a 256-byte aligned uint8 GPU tensor")
+        rc = lib.ns_int4_linear_splitk(out.data_ptr(), x2.data_ptr(), x2.stride(0),
+                                       qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
+                                       bias.data_ptr() if bias is not None else None, res_ptr, epilogue,
+                                       nw_ptr, float(norm_eps), M, N, K, group_size, _lib.DTYPE_CODES[x.dtype],
+                                       workspace.data_ptr(), workspace.numel(), stream)
+        _lib.check(rc, "ns_int4_linear_splitk")
+        return out.view(*lead, n_out)
     rc = lib.ns_int4_linear(out.data_ptr(), x2.data_ptr(), x2.stride(0),
                             qweight.data_ptr(), scales.data_ptr(), zeros.data_ptr(),
                             bias.data_ptr() if bias is not None else None, res_ptr, epilogue,
                             nw_ptr, float(norm_eps),
-                            M, N, K, group_size, _lib.DTYPE_CODES[x.dtype],
-                            torch.cuda.current_stream(x.device).cuda_stream)
+                            M, N, K, group_size, _lib.DTYPE_CODES[x.dtype], stream)
     _lib.check(rc, "ns_int4_linear")
     return out.view(*lead, n_out)
 
@@ -254,6 +273,10 @@ class Int4Linear(nn.Module):
         # rotary-pair order (rope_pairs); forward() then restores row order.
         self.rope_heads: tuple[int, int, int] | None = None
         self.rope_inverse: torch.Tensor | None = None
+        # Split-K workspace of long-K layers (allocated zeroed on first use; one
+        # module's calls run in stream order, so they never overlap).
+        self._splitk_ws: torch.Tensor | None = None
+        self._splitk_checked = False
 
     @classmethod
     def from_linear(cls, lin: nn.Linear, group_size: int = 128) -> "Int4Linear":
@@ -274,11 +297,16 @@ class Int4Linear(nn.Module):
             x, norm = norm(x), None
         if self.rope_heads is not None and residual is not None:
             raise ValueError("a rope-paired q|k|v projection takes no residual")
+        if not self._splitk_checked:
+            n = splitk_workspace_bytes(self.out_features, self.in_features)
+            self._splitk_ws = torch.zeros(n, dtype=torch.uint8, device=self.qweight.device) if n else None
+            self._splitk_checked = True
         y = int4_linear(x, self.qweight, self.scales, self.zeros,
                         None if self.bias is None else self.bias.data, self.group_size,
                         residual=residual, silu_mul=self.silu_mul,
                         norm_weight=None if norm is None else norm.weight.data,
-                        norm_eps=1e-6 if norm is None else norm.variance_epsilon)
+                        norm_eps=1e-6 if norm is None else norm.variance_epsilon,
+                        workspace=self._splitk_ws)
         return y if self.rope_inverse is None else y.index_select(-1, self.rope_inverse)
 
     @property

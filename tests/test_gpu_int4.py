@@ -354,3 +354,40 @@ def test_rope_cache_epilogue_matches_projection_then_rotary(dtype, M, heads, wit
         assert torch.equal(vc_a, vc_b), "value cache differs"
         # The module still returns rows in q|k|v order.
         assert torch.equal(paired(x, norm=norm), y)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 16, 33, 64, 100])
+def test_splitk_down_projection(dtype, M):
+    """ns_int4_linear_splitk on down_proj's shape (N 896, K 4864; 4 splits per tile
+    up to 16 tokens, 2 up to 32, none beyond): within one rounding of the oracle on
+    the residual epilogue, identical on a repeated call (the arrival counters are back
+    at zero), identical rows for a batch and its first row alone when both split the
+    same way, and within one rounding of the unsplit kernel."""
+    from nanoserve_amd.quant import splitk_workspace_bytes
+
+    N, K = 896, 4864
+    packed, s, z = (t.to(DEV) for t in _weights(N, K, 128, 71))
+    g = torch.Generator().manual_seed(72)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype)
+    res = torch.randn(M, N, generator=g).to(dtype)
+    ws = torch.zeros(splitk_workspace_bytes(N, K), dtype=torch.uint8, device=DEV)
+    assert ws.numel() > 0
+    xd, bd, rd = x.to(DEV), b.to(DEV), res.to(DEV)
+    first = int4_linear(xd, packed, s, z, bd, 128, residual=rd, workspace=ws)
+    again = int4_linear(xd, packed, s, z, bd, 128, residual=rd, workspace=ws)
+    plain = int4_linear(xd, packed, s, z, bd, 128, residual=rd)
+    head = int4_linear(xd[:1].contiguous(), packed, s, z, bd, 128, residual=rd[:1].contiguous(), workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    if M <= 16:  # same split count as the one-row launch: the batch does not change a row's sums
+        assert torch.equal(head, first[:1])
+    assert not ws[:256].any(), "arrival counters must be left at zero"
+    w = dequantize_int4_ref(packed.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(), 128, NAME[dtype])
+    y = int4_linear_ref(x.float().numpy(), w, b.float().numpy())
+    want = _round(y, dtype) + res.double().numpy()
+    tol = 2 * RTOL[dtype] * (np.abs(y) + np.abs(res.double().numpy())) + 1e-5
+    for t in (first, plain):
+        err = np.abs(t.double().cpu().numpy() - want)
+        assert (err <= tol).all(), f"max err {err.max():.3e}"
