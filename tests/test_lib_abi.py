@@ -178,6 +178,41 @@ def test_int4_linear_rejects_bad_arguments(over, code):
     assert lib.ns_int4_linear(*_i4_args(**over)) == code
 
 
+def test_int4_linear_splitk_checks_its_workspace():
+    """down_proj's shape splits (a workspace is required and sized by the query);
+    a shape that does not split needs none.  Rejected before any launch."""
+    lib = _lib.load()
+    M, N, K = 16, 896, 4864
+    need = lib.ns_int4_linear_splitk_workspace_size(M, N, K)
+    assert need > 0 and lib.ns_int4_linear_splitk_workspace_size(16, 64, 256) == 0
+    assert lib.ns_int4_linear_splitk_workspace_size(-1, N, K) == 0
+    base = _i4_args(M=M, N=N, K=K, xs=K)[:-1]
+    for ws, nbytes in ((None, need), (256, need - 1), (128, need)):  # missing, too small, misaligned
+        assert lib.ns_int4_linear_splitk(*base, ws, nbytes, None) == _lib.NS_ERR_INVALID_ARG
+    assert lib.ns_int4_linear_splitk(*_i4_args(M=M, N=N, K=K, xs=K, x=None)[:-1], 256, need, None) == \
+        _lib.NS_ERR_INVALID_ARG
+
+
+def test_int4_linear_rope_cache_rejects_bad_arguments():
+    lib = _lib.load()
+
+    def call(**over):
+        a = dict(q=16, x=16, xs=896, qw=16, sc=16, zp=16, bias=None, nw=None, eps=1e-6, cos=16, sin=16, css=64,
+                 kc=16, vc=16, slots=16, s64=1, M=4, K=896, gs=128, hq=14, hkv=2, d=64, bs=16, nb=8,
+                 dt=_lib.NS_DTYPE_F16, stream=None)
+        a.update(over)
+        return lib.ns_int4_linear_rope_cache(*a.values())
+
+    assert call(M=0, x=None) == _lib.NS_OK
+    assert call(dt=_lib.NS_DTYPE_F32) == _lib.NS_ERR_UNSUPPORTED
+    assert call(d=40) == _lib.NS_ERR_UNSUPPORTED           # head_dim not a multiple of 16
+    assert call(K=2048, xs=2048) == _lib.NS_ERR_UNSUPPORTED  # more than 8 chunks
+    assert call(kc=None) == _lib.NS_ERR_INVALID_ARG
+    assert call(cos=20) == _lib.NS_ERR_INVALID_ARG         # cos/sin rows read as 8-byte vectors
+    assert call(css=62) == _lib.NS_ERR_INVALID_ARG
+    assert call(hkv=0) == _lib.NS_ERR_INVALID_ARG
+
+
 def test_int4_linear_zero_rows_is_a_no_op():
     lib = _lib.load()
     assert lib.ns_int4_linear(*_i4_args(M=0, x=None)) == _lib.NS_OK
