@@ -665,8 +665,17 @@ __global__ __launch_bounds__(256) void int4_dequantize_kernel(typename DT::T* ou
 namespace ns {
 namespace {
 
-// Split-K workspace: one u32 arrival counter per tile (zero between calls),
-// padded to 256 bytes, then the partial sums, 16 bytes per lane, tile and split.
+// Split-K workspace: a fixed region of u32 arrival counters (one per tile,
+// zero between calls), then the partial sums, 16 bytes per lane, tile and
+// split.  The region has the same size for every M: a tile only splits when
+// 2 * tiles <= 256, so at most 128 counters exist, and the partials of any
+// call start past every counter any other call may use.  One workspace can
+// therefore serve calls of every token count in turn (a layer's decode steps
+// change M from step to step) without a call's partial sums landing on
+// another call's counters.
+constexpr int64_t kSplitkMaxTiles = 128;
+constexpr int64_t kSplitkCounterBytes = kSplitkMaxTiles * 4;
+
 struct SplitkLayout {
   int splits;
   int64_t counter_bytes, part_bytes;
@@ -677,10 +686,11 @@ SplitkLayout splitk_layout(int64_t M, int N, int K) {
   const int64_t tiles = static_cast<int64_t>(N / 16) * ((M + mt - 1) / mt);
   SplitkLayout l;
   l.splits = M > 0 ? splitk_for(N, K, (M + mt - 1) / mt) : 1;
-  l.counter_bytes = l.splits > 1 ? (tiles * 4 + 255) / 256 * 256 : 0;
+  l.counter_bytes = l.splits > 1 ? kSplitkCounterBytes : 0;
   l.part_bytes = l.splits > 1 ? tiles * l.splits * (mt / 16) * 64 * 16 : 0;
   return l;
 }
+static_assert(kSplitkCounterBytes % 256 == 0, "partials stay 256-byte aligned");
 
 int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void* qweight, const void* scales,
                       const void* zeros, const void* bias, const void* residual, int epilogue,

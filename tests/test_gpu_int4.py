@@ -23,6 +23,9 @@ RTOL = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
 
 # Qwen2.5-0.5B projections (in -> out): q, k/v, o, gate/up, down, and fused q|k|v, gate|up.
+# Arrival-counter region at the head of every split-K workspace (128 tiles x u32).
+SPLITK_COUNTER_BYTES = 512
+
 QWEN = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 1152), (896, 9728)]
 
 
@@ -359,8 +362,9 @@ def test_rope_cache_epilogue_matches_projection_then_rotary(dtype, M, heads, wit
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("M", [1, 16, 33, 64, 100])
 def test_splitk_down_projection(dtype, M):
-    """ns_int4_linear_splitk on down_proj's shape (N 896, K 4864; 4 splits per tile
-    up to 16 tokens, 2 up to 32, none beyond): within one rounding of the oracle on
+    """ns_int4_linear_splitk on down_proj's shape (N 896, K 4864; 4 splits per
+    16-token tile up to 16 tokens, 2 up to 32, none at 33-64; beyond 64 tokens the
+    tiles are 64 tokens wide and split twice again): within one rounding of the oracle on
     the residual epilogue, identical on a repeated call (the arrival counters are back
     at zero), identical rows for a batch and its first row alone when both split the
     same way, and within one rounding of the unsplit kernel."""
@@ -383,7 +387,7 @@ def test_splitk_down_projection(dtype, M):
     assert torch.equal(first, again)
     if M <= 16:  # same split count as the one-row launch: the batch does not change a row's sums
         assert torch.equal(head, first[:1])
-    assert not ws[:256].any(), "arrival counters must be left at zero"
+    assert not ws[:SPLITK_COUNTER_BYTES].any(), "arrival counters must be left at zero"
     w = dequantize_int4_ref(packed.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(), 128, NAME[dtype])
     y = int4_linear_ref(x.float().numpy(), w, b.float().numpy())
     want = _round(y, dtype) + res.double().numpy()
@@ -391,3 +395,31 @@ def test_splitk_down_projection(dtype, M):
     for t in (first, plain):
         err = np.abs(t.double().cpu().numpy() - want)
         assert (err <= tol).all(), f"max err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_splitk_workspace_reused_across_token_counts(dtype):
+    """One split-K workspace serves down_proj calls whose token counts change from
+    call to call, as a layer's decode steps do (M = 1, 32, 100, 1, 17, 8): each call
+    equals, bit for bit, the same call on a fresh zeroed workspace, and the whole
+    arrival-counter region is back at zero after every call.  A small-M call's
+    partial sums must never land where a larger-M call keeps its counters."""
+    from nanoserve_amd.quant import splitk_workspace_bytes
+
+    N, K = 896, 4864
+    packed, s, z = (t.to(DEV) for t in _weights(N, K, 128, 81))
+    nbytes = splitk_workspace_bytes(N, K)
+    shared = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    g = torch.Generator().manual_seed(82)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype).to(DEV)
+    for M in (1, 32, 100, 1, 17, 8, 32):
+        print(f"splitk reuse M={M} {dtype}", flush=True)
+        x = torch.randn(M, K, generator=g).to(dtype).to(DEV)
+        res = torch.randn(M, N, generator=g).to(dtype).to(DEV)
+        got = int4_linear(x, packed, s, z, b, 128, residual=res, workspace=shared)
+        fresh_ws = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+        want = int4_linear(x, packed, s, z, b, 128, residual=res, workspace=fresh_ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"M={M}: reused workspace differs from a fresh one"
+        assert not shared[:SPLITK_COUNTER_BYTES].any(), f"M={M}: counters left non-zero"
+        assert not fresh_ws[:SPLITK_COUNTER_BYTES].any()
