@@ -23,6 +23,9 @@
  *
  * Every function returns NS_OK (0) or a negative NS_ERR_* code and never
  * aborts the process.  Argument checks run on the host before any HIP call.
+ * The library creates no streams, events or device allocations of its own:
+ * a mixed batch that should overlap its decode and prefill launches gets a
+ * second stream and two events from the caller (ns_paged_attention).
  */
 #ifndef NANOSERVE_PAGED_H
 #define NANOSERVE_PAGED_H
@@ -236,6 +239,16 @@ int ns_argmax_rows(int64_t* out, const void* x, int64_t x_stride_row, int64_t M,
                    int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * ns_stream_read -- measurement floor, no counterpart in the reference: read
+ * `bytes` (a multiple of 16, src 16-byte aligned) with 16-byte loads over
+ * `grid` workgroups of 256 threads, each writing the XOR of what it read to
+ * out[workgroup] (grid 32-bit words).  With bytes == 0 the launch does no
+ * reads: the cost of an empty launch.  The benchmark's floors mode times it
+ * next to the attention kernels.
+ */
+int ns_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void* stream);
+
+/*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
  * ns_paged_attention needs for these sizes (split-K partials and counters).
  * Without is_decode_only it includes the prefill split state: a fixed 512
@@ -294,6 +307,15 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  * length (never by the block-table width), so zero-padded table rows are
  * safe.  A block id outside [0, num_blocks) is never dereferenced; the
  * affected (sequence, head) outputs are written as NaN.
+ *
+ * aux_stream, fork_event, join_event (optional: all three or none, owned by
+ * the caller; aux_stream must differ from stream).  With them, a batch that
+ * has both decode rows and prefill rows forks the decode launch onto
+ * aux_stream (fork_event recorded on stream, waited on by aux_stream) and
+ * joins it back (join_event recorded on aux_stream, waited on by stream), so
+ * the two launches overlap; graph capture records both dependencies.  Without
+ * them both launches run in order on stream.  Decode-only and prefill-only
+ * batches never touch them.  Calls that overlap in time need their own set.
  */
 int ns_paged_attention(void* out, const void* query,
                        const void* k_cache, const void* v_cache,
@@ -308,7 +330,8 @@ int ns_paged_attention(void* out, const void* query,
                        int num_heads, int num_kv_heads, int head_dim,
                        int block_size, int64_t num_blocks,
                        float scale, int dtype,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       void* workspace, size_t workspace_bytes, void* stream,
+                       void* aux_stream, void* fork_event, void* join_event);
 
 #ifdef __cplusplus
 }

@@ -55,16 +55,50 @@ _INDEX_DTYPES = (torch.int32, torch.int64)
 # overlap in time and therefore get different buffers.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 
+# Per (device, stream): the second stream and fork/join events a mixed batch
+# overlaps its decode launch on.  The shim owns them; the library only uses
+# what it is handed.
+_aux: dict[tuple[int, int], tuple[torch.cuda.Stream, torch.cuda.Event, torch.cuda.Event]] = {}
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
+
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    key = (_device_index(device), stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            # A graph captured with the old buffer would keep its freed
+            # address, and the new buffer's zero fill would be recorded into
+            # this graph.  Callers warm up every shape before capturing.
+            raise RuntimeError(
+                f"paged attention needs a {nbytes}-byte workspace on stream {stream:#x} during graph "
+                f"capture, but has {0 if ws is None else ws.numel()} bytes: run the largest shape "
+                "once on this stream before capturing")
         # Grow geometrically so a slowly growing max_seq_len reallocates rarely.
         size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
+
+
+def _aux_stream(device: torch.device, stream: int):
+    """(aux stream, fork event, join event) handles for overlapping a mixed batch."""
+    key = (_device_index(device), stream)
+    aux = _aux.get(key)
+    if aux is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None, None, None  # created on first use outside capture; run in order meanwhile
+        side = torch.cuda.Stream(device)  # default priority
+        fork, join = torch.cuda.Event(), torch.cuda.Event()
+        fork.record(side)  # creates the HIP events (torch creates them lazily)
+        join.record(side)
+        side.synchronize()
+        aux = _aux[key] = (side, fork, join)
+    side, fork, join = aux
+    return side.cuda_stream, fork.cuda_event, join.cuda_event
 
 
 def _index(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
@@ -162,6 +196,7 @@ def paged_attention_hip(
             f"unsupported attention shape: Hq={num_heads} Hkv={num_kv_heads} D={head_dim} "
             f"block_size={block_size}")
     ws = _workspace(device, stream, nbytes)
+    aux = (None, None, None) if decode_only else _aux_stream(device, stream)
 
     rc = lib.ns_paged_attention(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -173,7 +208,7 @@ def paged_attention_hip(
         md.num_seqs, num_tokens, md.max_query_len, md.max_seq_len, int(decode_only),
         num_heads, num_kv_heads, head_dim, block_size, num_blocks,
         float(scale), _lib.DTYPE_CODES[q.dtype],
-        ws.data_ptr(), ws.numel(), stream)
+        ws.data_ptr(), ws.numel(), stream, *aux)
     _lib.check(rc, "ns_paged_attention")
     return out.view(query.shape)
 

@@ -19,7 +19,6 @@
 #include <math.h>
 
 #include <algorithm>
-#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -1138,50 +1137,24 @@ int64_t round_up_ctx(int max_seq_len, int block_size) {
 }
 
 
-// A mixed batch runs its decode rows on a side stream, forked from and joined
-// back to the caller's stream with events, so the memory-bound decode kernel
-// overlaps the compute-bound prefill kernel.  One side stream (default
-// priority) and event pair per device, created on first use outside graph
-// capture; the fork/join is an ordinary cross-stream dependency, which graph
-// capture records as such.  Without them the two launches run in order on
-// the caller's stream.
-struct SideStream {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-  bool failed = false;
+// The caller's secondary stream and fork/join events of a mixed batch
+// (all three, or none).  The library owns none of them.
+struct AuxStream {
+  hipStream_t stream;
+  hipEvent_t fork, join;
 };
-constexpr int kMaxDevices = 64;
-std::mutex g_side_mu;
-SideStream g_side[kMaxDevices];
-
-SideStream* side_stream_for(hipStream_t st) {
-  int dev = -1, sdev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  if (st != nullptr && (hipStreamGetDevice(st, &sdev) != hipSuccess || sdev != dev)) return nullptr;
-  SideStream& ss = g_side[dev];
-  if (ss.stream) return &ss;
-  if (ss.failed) return nullptr;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
-  if (hipStreamCreateWithFlags(&ss.stream, hipStreamNonBlocking) != hipSuccess) ss.stream = nullptr;
-  if (ss.stream && hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming) != hipSuccess) ss.fork = nullptr;
-  if (ss.fork && hipEventCreateWithFlags(&ss.join, hipEventDisableTiming) != hipSuccess) ss.join = nullptr;
-  if (!ss.join) {
-    if (ss.fork) (void)hipEventDestroy(ss.fork);
-    if (ss.stream) (void)hipStreamDestroy(ss.stream);
-    ss = SideStream{};
-    ss.failed = true;
-    return nullptr;
-  }
-  return &ss;
-}
 
 // Launch the decode kernel with `p` and, unless the batch is decode-only,
 // the prefill kernel with `pp` (its own plan); `launch_decode` is false when
-// the host query offsets show no one-row sequence.
+// the host query offsets show no one-row sequence.  A mixed batch with an aux
+// stream runs its decode rows there, forked from and joined back to `stream`
+// with the caller's events, so the memory-bound decode kernel overlaps the
+// compute-bound prefill kernel; graph capture records the fork and join as
+// ordinary cross-stream dependencies.  Without one the two launches run in
+// order on `stream`.
 template <class DT, int D>
 hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool launch_decode, int num_seqs,
-                            int max_query_len, hipStream_t stream) {
+                            int max_query_len, hipStream_t stream, const AuxStream* aux) {
   void* args[] = {&p};
   void* pargs[] = {&pp};
   constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
@@ -1213,22 +1186,20 @@ hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool l
   }
   if (!launch_decode) return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
 
-  std::lock_guard<std::mutex> lock(g_side_mu);
-  SideStream* ss = side_stream_for(stream);
-  if (!ss) {
+  if (!aux) {
     hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
     if (e != hipSuccess) return e;
     return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
   }
-  hipError_t e = hipEventRecord(ss->fork, stream);
-  if (e == hipSuccess) e = hipStreamWaitEvent(ss->stream, ss->fork, 0);
+  hipError_t e = hipEventRecord(aux->fork, stream);
+  if (e == hipSuccess) e = hipStreamWaitEvent(aux->stream, aux->fork, 0);
   if (e != hipSuccess) return e;
-  // Once the side stream depends on the caller's, it is joined back whatever
+  // Once the aux stream depends on the caller's, it is joined back whatever
   // else fails (an unjoined fork would also break a graph capture).
-  const hipError_t ed = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, ss->stream);
-  const hipError_t er = hipEventRecord(ss->join, ss->stream);
+  const hipError_t ed = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, aux->stream);
+  const hipError_t er = hipEventRecord(aux->join, aux->stream);
   const hipError_t ev = hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
-  const hipError_t ej = er == hipSuccess ? hipStreamWaitEvent(stream, ss->join, 0) : er;
+  const hipError_t ej = er == hipSuccess ? hipStreamWaitEvent(stream, aux->join, 0) : er;
   return ed != hipSuccess ? ed : (ev != hipSuccess ? ev : ej);
 }
 
@@ -1501,7 +1472,8 @@ extern "C" int ns_paged_attention(void* out, const void* query,
                                   int num_heads, int num_kv_heads, int head_dim,
                                   int block_size, int64_t num_blocks,
                                   float scale, int dtype,
-                                  void* workspace, size_t workspace_bytes, void* stream) {
+                                  void* workspace, size_t workspace_bytes, void* stream,
+                                  void* aux_stream, void* fork_event, void* join_event) {
   using namespace ns;
   if (num_seqs < 0 || num_tokens < 0) return NS_ERR_INVALID_ARG;
   if (num_seqs == 0 || num_tokens == 0) return NS_OK;
@@ -1525,6 +1497,12 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   if (num_seqs > 65535 || num_kv_heads > 65535) return NS_ERR_UNSUPPORTED;
   if (!aligned16(out) || !aligned16(query) || !aligned16(k_cache) || !aligned16(v_cache))
     return NS_ERR_INVALID_ARG;
+  // The aux stream comes with both events or not at all.
+  const int aux_given = (aux_stream != nullptr) + (fork_event != nullptr) + (join_event != nullptr);
+  if (aux_given != 0 && aux_given != 3) return NS_ERR_INVALID_ARG;
+  if (aux_given && aux_stream == stream) return NS_ERR_INVALID_ARG;
+  const AuxStream aux{static_cast<hipStream_t>(aux_stream), static_cast<hipEvent_t>(fork_event),
+                      static_cast<hipEvent_t>(join_event)};
 
   const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
   const DecodePlan plan = plan_decode(head_dim, ctx_plan);
@@ -1598,12 +1576,13 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   }
 
   hipStream_t st = static_cast<hipStream_t>(stream);
+  const AuxStream* ax = aux_given ? &aux : nullptr;
   hipError_t e;
   if (dtype == NS_DTYPE_F16)
-    e = head_dim == 64 ? launch_attention<F16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st)
-                       : launch_attention<F16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st);
+    e = head_dim == 64 ? launch_attention<F16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
+                       : launch_attention<F16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
   else
-    e = head_dim == 64 ? launch_attention<BF16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st)
-                       : launch_attention<BF16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st);
+    e = head_dim == 64 ? launch_attention<BF16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
+                       : launch_attention<BF16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }

@@ -299,6 +299,12 @@ class Int4Linear(nn.Module):
             raise ValueError("a rope-paired q|k|v projection takes no residual")
         if not self._splitk_checked:
             n = splitk_workspace_bytes(self.out_features, self.in_features)
+            if n and torch.cuda.is_current_stream_capturing():
+                # The zero fill would be recorded into the graph (and rerun by
+                # every replay); the first call belongs before capture.
+                raise RuntimeError(
+                    f"Int4Linear({self.in_features}, {self.out_features}) allocates its split-K workspace "
+                    "on first use: call it once before graph capture")
             self._splitk_ws = torch.zeros(n, dtype=torch.uint8, device=self.qweight.device) if n else None
             self._splitk_checked = True
         y = int4_linear(x, self.qweight, self.scales, self.zeros,

@@ -20,6 +20,13 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            # A graph captured earlier with the old buffer would keep its freed
+            # address; callers warm up every shape before capturing.
+            raise RuntimeError(
+                f"argmax_rows needs a {nbytes}-byte workspace on stream {stream:#x} during graph "
+                f"capture, but has {0 if ws is None else ws.numel()} bytes: run the largest shape "
+                "once on this stream before capturing")
         ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

@@ -380,8 +380,8 @@ def test_graph_replays_match_eager(config):
 
     Eager calls run between replays, so the split-K counters a replay leaves
     behind are exercised by the eager path and the other way round.  The mixed
-    c3 batch forks its decode rows onto the library's side stream, so its
-    capture records the fork and the join.
+    c3 batch forks its decode rows onto the shim's aux stream, so its capture
+    records the fork and the join.
     """
     case = make_case(config, seed=5, device=DEV, gen_device=DEV)
     eager = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale).clone()
