@@ -11,7 +11,7 @@ write with hand-written gfx950 HIP kernels behind a C ABI
 """
 
 from .attention import AttentionMetadata, get_attention_backend, paged_attention_hip
-from .block_manager import BlockAllocator, BlockSpaceManager
+from .block_manager import BlockSpaceManager
 from .kv_cache import PagedKVCache, kv_bytes_per_token, reshape_and_cache
 from .rotary import RotaryEmbedding, rope_reshape_and_cache
 
@@ -19,7 +19,6 @@ __version__ = "0.1.0"
 
 __all__ = [
     "AttentionMetadata",
-    "BlockAllocator",
     "BlockSpaceManager",
     "PagedKVCache",
     "get_attention_backend",

@@ -1,29 +1,20 @@
 """A minimal continuous-batching engine around the HIP path.
 
-Enough of the reference engine (nanoserve/engine.py, scheduler.py,
-sequence.py, model_runner.py, metrics.py) to run the end-to-end serving
-benchmark with the kernels inside the model: requests join and leave the
-batch every step, prefill and decode share one token budget, long prompts are
-prefilled in chunks, and when blocks run out the newest running sequence is
-preempted and later recomputed.  Sampling is greedy (the benchmark's setting).
-
-The scheduling rules follow the reference:
-  * running sequences are served first, oldest first, then waiting requests
-    are admitted while budget, sequence slots and blocks last
-    (scheduler.py:91-202);
-  * a sequence that cannot get blocks evicts the newest running sequence not
-    yet granted tokens this step (scheduler.py:204-262);
-  * a step's metadata is built in scheduler order with int64 indices in one
-    host-to-device copy (model_runner.py:52-147); a sequence yields a token
-    only in the step that computes its last uncomputed token.
+Enough of the reference engine (nanoserve/engine.py, model_runner.py,
+metrics.py) to run the end-to-end serving benchmark with the kernels inside
+the model: requests join and leave the batch every step, prefill and decode
+share one token budget, long prompts are prefilled in chunks, and when
+blocks run out sequences are evicted and later recomputed (the scheduling
+rules live in `scheduling.py`).  Sampling is greedy (the benchmark's
+setting).  A step's metadata is built in scheduler order with int64 indices
+in one host-to-device copy (model_runner.py:52-147); a sequence yields a
+token only in the step that computes its last uncomputed token.
 """
 
 from __future__ import annotations
 
-import enum
 import time
-from collections import deque
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -32,287 +23,10 @@ from .attention import AttentionMetadata, get_attention_backend
 from .block_manager import BlockSpaceManager
 from .kv_cache import PagedKVCache
 from .sampling import argmax_rows
+from .scheduling import RequestMetrics, SamplingParams, Scheduler, SchedulerConfig, Sequence, SeqState
 
-
-@dataclass
-class SamplingParams:
-    max_new_tokens: int = 16
-    ignore_eos: bool = False
-
-
-@dataclass
-class SchedulerConfig:
-    max_num_batched_tokens: int = 2048
-    max_num_seqs: int = 64
-    enable_chunked_prefill: bool = True
-    # "recompute": evict the newest running sequence and re-prefill it later;
-    # "none": running out of KV blocks raises instead of stalling (the
-    # reference's ablation mode, config.py:82, scheduler.py:205-252).
-    preemption_mode: str = "recompute"
-
-
-class SeqStatus(enum.Enum):
-    WAITING = enum.auto()
-    RUNNING = enum.auto()
-    PREEMPTED = enum.auto()
-    FINISHED_LENGTH = enum.auto()
-    FINISHED_EOS = enum.auto()
-
-    @property
-    def finished(self) -> bool:
-        return self in (SeqStatus.FINISHED_LENGTH, SeqStatus.FINISHED_EOS)
-
-
-@dataclass
-class RequestMetrics:
-    """Per-request timestamps (reference metrics.py:10-38)."""
-
-    request_id: int
-    prompt_tokens: int
-    arrival: float
-    start: float = 0.0
-    first_token: float = 0.0
-    end: float = 0.0
-    output_tokens: int = 0
-
-    @property
-    def ttft(self) -> float:
-        return self.first_token - self.arrival
-
-    @property
-    def e2e(self) -> float:
-        return self.end - self.arrival
-
-    @property
-    def tpot(self) -> float:
-        """Mean seconds per output token after the first."""
-        if self.output_tokens <= 1:
-            return 0.0
-        return (self.end - self.first_token) / (self.output_tokens - 1)
-
-
-@dataclass(eq=False)
-class Sequence:
-    """One request's state; num_computed_tokens marks how much of it has KV in the cache."""
-
-    seq_id: int
-    prompt_token_ids: list[int]
-    sampling: SamplingParams
-    arrival: float = field(default_factory=time.perf_counter)
-    output_token_ids: list[int] = field(default_factory=list)
-    status: SeqStatus = SeqStatus.WAITING
-    block_table: list[int] = field(default_factory=list)
-    num_computed_tokens: int = 0
-    num_preemptions: int = 0
-    metrics: RequestMetrics | None = None
-
-    def __post_init__(self) -> None:
-        if self.metrics is None:
-            self.metrics = RequestMetrics(self.seq_id, len(self.prompt_token_ids), self.arrival)
-
-    @property
-    def prompt_len(self) -> int:
-        return len(self.prompt_token_ids)
-
-    @property
-    def num_tokens(self) -> int:
-        return len(self.prompt_token_ids) + len(self.output_token_ids)
-
-    @property
-    def num_uncomputed_tokens(self) -> int:
-        return self.num_tokens - self.num_computed_tokens
-
-    @property
-    def is_prefilling(self) -> bool:
-        return self.num_computed_tokens < self.prompt_len
-
-    def slice_token_ids(self, start: int, end: int) -> list[int]:
-        p = self.prompt_len
-        if end <= p:
-            return self.prompt_token_ids[start:end]
-        if start >= p:
-            return self.output_token_ids[start - p:end - p]
-        return self.prompt_token_ids[start:] + self.output_token_ids[:end - p]
-
-    def advance_computed(self, n: int) -> None:
-        self.num_computed_tokens += n
-        assert self.num_computed_tokens <= self.num_tokens
-
-    def reset_for_recompute(self) -> None:
-        self.block_table = []
-        self.num_computed_tokens = 0
-        self.status = SeqStatus.PREEMPTED
-        self.num_preemptions += 1
-
-    def check_stop(self, eos_token_id: int | None) -> bool:
-        if len(self.output_token_ids) >= self.sampling.max_new_tokens:
-            self.status = SeqStatus.FINISHED_LENGTH
-            return True
-        if (not self.sampling.ignore_eos and eos_token_id is not None and self.output_token_ids
-                and self.output_token_ids[-1] == eos_token_id):
-            self.status = SeqStatus.FINISHED_EOS
-            return True
-        return False
-
-
-@dataclass
-class SchedulerOutput:
-    scheduled: list = field(default_factory=list)  # [(Sequence, num_tokens)]
-    preempted: list = field(default_factory=list)
-    num_batched_tokens: int = 0
-    num_prefill_seqs: int = 0
-    num_decode_seqs: int = 0
-
-    def __bool__(self) -> bool:
-        return bool(self.scheduled)
-
-
-@dataclass
-class SchedulerStats:
-    """Running totals over the scheduler's life (reference scheduler.py:55-66)."""
-
-    total_steps: int = 0
-    total_preemptions: int = 0
-    total_prefill_tokens: int = 0
-    total_decode_tokens: int = 0
-    batch_size_sum: int = 0
-    mixed_steps: int = 0
-
-    @property
-    def mean_batch_size(self) -> float:
-        return self.batch_size_sum / self.total_steps if self.total_steps else 0.0
-
-
-class Scheduler:
-    def __init__(self, cfg: SchedulerConfig, block_manager: BlockSpaceManager) -> None:
-        if cfg.preemption_mode not in ("recompute", "none"):
-            raise ValueError(f"unknown preemption_mode {cfg.preemption_mode!r}")
-        self.cfg = cfg
-        self.block_manager = block_manager
-        self.waiting: deque[Sequence] = deque()
-        self.running: list[Sequence] = []
-        self.stats = SchedulerStats()
-
-    @property
-    def num_preemptions(self) -> int:
-        return self.stats.total_preemptions
-
-    def add(self, seq: Sequence) -> None:
-        seq.status = SeqStatus.WAITING
-        self.waiting.append(seq)
-
-    @property
-    def has_work(self) -> bool:
-        return bool(self.waiting or self.running)
-
-    def schedule(self) -> SchedulerOutput:
-        out = SchedulerOutput()
-        budget = self._schedule_running(out, self.cfg.max_num_batched_tokens)
-        self._schedule_waiting(out, budget)
-        # Counted before the runner advances num_computed_tokens, while
-        # is_prefilling still says what this step does for each sequence.
-        for seq, q in out.scheduled:
-            if seq.is_prefilling:
-                out.num_prefill_seqs += 1
-                self.stats.total_prefill_tokens += q
-            else:
-                out.num_decode_seqs += 1
-                self.stats.total_decode_tokens += q
-            out.num_batched_tokens += q
-        if out.scheduled:
-            self.stats.total_steps += 1
-            self.stats.batch_size_sum += len(out.scheduled)
-            self.stats.mixed_steps += bool(out.num_prefill_seqs and out.num_decode_seqs)
-        return out
-
-    def _schedule_running(self, out: SchedulerOutput, budget: int) -> int:
-        snapshot = list(self.running)
-        still_running: list[Sequence] = []
-        protected: set[int] = set()
-        for seq in snapshot:
-            if seq.status is not SeqStatus.RUNNING:
-                continue  # evicted earlier in this step
-            if budget <= 0:
-                still_running.append(seq)
-                continue
-            want = min(seq.num_uncomputed_tokens, budget)
-            if not self.cfg.enable_chunked_prefill and seq.is_prefilling:
-                want = seq.num_uncomputed_tokens
-                if want > budget:
-                    still_running.append(seq)
-                    continue
-            need = seq.num_computed_tokens + want
-            admitted = True
-            while not self.block_manager.allocate(seq, need):
-                victim = None if self.cfg.preemption_mode == "none" else next(
-                    (s for s in reversed(snapshot)
-                     if s.status is SeqStatus.RUNNING and s.seq_id not in protected and s is not seq), None)
-                if victim is None:
-                    cap = self.block_manager.num_total_blocks - self.block_manager.watermark_blocks
-                    if self.block_manager.blocks_for(need) > cap:
-                        raise ValueError(f"request {seq.seq_id} needs {self.block_manager.blocks_for(need)} "
-                                         f"KV blocks but the cache holds {cap}")
-                    if self.cfg.preemption_mode == "none":
-                        # Without eviction nothing can free a block: say so
-                        # rather than stall (reference scheduler.py:222-252).
-                        raise RuntimeError(f"out of KV blocks at request {seq.seq_id} with preemption disabled: "
-                                           f"{len(snapshot)} running sequences hold all "
-                                           f"{self.block_manager.num_total_blocks} blocks")
-                    # Last one standing: it goes back to the queue and retries.
-                    self._preempt(seq, out)
-                    admitted = False
-                    break
-                self._preempt(victim, out)
-                if victim in still_running:
-                    still_running.remove(victim)
-            if admitted:
-                out.scheduled.append((seq, want))
-                protected.add(seq.seq_id)
-                budget -= want
-                still_running.append(seq)
-        self.running = still_running
-        return budget
-
-    def _schedule_waiting(self, out: SchedulerOutput, budget: int) -> int:
-        just_preempted = {s.seq_id for s in out.preempted}
-        while self.waiting and budget > 0 and len(self.running) < self.cfg.max_num_seqs:
-            seq = self.waiting[0]
-            if seq.seq_id in just_preempted:
-                break
-            want = min(seq.num_uncomputed_tokens, budget)
-            if not self.cfg.enable_chunked_prefill:
-                want = seq.num_uncomputed_tokens
-                if want > self.cfg.max_num_batched_tokens:
-                    raise ValueError(f"prompt of {want} tokens exceeds max_num_batched_tokens; "
-                                     "enable chunked prefill")
-                if want > budget:
-                    break
-            need = seq.num_computed_tokens + want
-            if not self.block_manager.can_allocate(seq, need) or not self.block_manager.allocate(seq, need):
-                break
-            self.waiting.popleft()
-            seq.status = SeqStatus.RUNNING
-            if seq.metrics.start == 0.0:
-                seq.metrics.start = time.perf_counter()
-            self.running.append(seq)
-            out.scheduled.append((seq, want))
-            budget -= want
-        return budget
-
-    def _preempt(self, seq: Sequence, out: SchedulerOutput) -> None:
-        """Newest-first eviction by recompute: free the blocks, requeue at the front."""
-        self.block_manager.free(seq)
-        seq.reset_for_recompute()
-        self.stats.total_preemptions += 1
-        out.preempted.append(seq)
-        self.waiting.appendleft(seq)
-
-    def free_finished(self) -> list[Sequence]:
-        done = [s for s in self.running if s.status.finished]
-        for s in done:
-            self.block_manager.free(s)
-        self.running = [s for s in self.running if not s.status.finished]
-        return done
+__all__ = ["DecodeGraphs", "LLMEngine", "ModelRunner", "RequestMetrics", "SamplingParams", "Scheduler",
+           "SchedulerConfig", "Sequence", "SeqState", "summarize"]
 
 
 class ModelRunner:
@@ -360,7 +74,7 @@ class ModelRunner:
         sample_indices, sample_seqs = [], []
         for seq, q in scheduled:
             start, end = seq.num_computed_tokens, seq.num_computed_tokens + q
-            input_ids.extend(seq.slice_token_ids(start, end))
+            input_ids.extend(seq.token_slice(start, end))
             positions.extend(range(start, end))
             slots.extend(self.block_manager.slot_mapping(seq, start, end))
             qsl.append(qsl[-1] + q)
@@ -394,7 +108,7 @@ class ModelRunner:
         ids, pos, md, sample_idx, sample_seqs = self.build_inputs(scheduled)
         hidden = self.model(ids, pos, self.kv_cache, md, self.attn_fn)
         for seq, q in scheduled:
-            seq.advance_computed(q)
+            seq.mark_computed(q)
         if sample_idx is None:
             return []
         logits = self.model.compute_logits(hidden, sample_idx)
@@ -598,7 +312,7 @@ class DecodeGraphs:
         launch = self.launch(scheduled)
         tokens = self.tokens(launch)
         for seq, q in scheduled:
-            seq.advance_computed(q)
+            seq.mark_computed(q)
         return [(seq, tok) for (seq, _), tok in zip(scheduled, tokens)]
 
 
@@ -670,7 +384,7 @@ class LLMEngine:
         for seq, tok in results:
             seq.output_token_ids.append(tok)
             self._record(seq, now)
-            seq.check_stop(self.eos_token_id)
+            seq.check_done(self.eos_token_id)
         done = self.scheduler.free_finished()
         self.finished.extend(done)
         return done
@@ -687,10 +401,10 @@ class LLMEngine:
         held: list[int] = []
         if pending is not None:
             for seq, _ in pending.scheduled:
-                seq.advance_computed(1)
+                seq.mark_computed(1)
                 seq.output_token_ids.append(-1)  # placeholder until the tokens are read back
                 held.append(len(seq.output_token_ids) - 1)
-                seq.check_stop(None)
+                seq.check_done(None)
             done = self.scheduler.free_finished()
             self.finished.extend(done)
         sched = self.scheduler.schedule()

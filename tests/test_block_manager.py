@@ -3,7 +3,7 @@
 The slot mapping is the cache write's addressing contract: an off-by-one
 silently reads or overwrites another sequence's KV.  These tests cover the
 behaviours the reference pins for its block manager (reference
-tests/test_block_manager.py:22-171): allocator round trips and failures,
+tests/test_block_manager.py:22-171): allocation round trips and failures,
 incremental growth, the watermark, the closed-form slot formula
 (block_manager.py:131-132), contiguity inside a block, the decode step's slot,
 running past the table, and no aliasing between live sequences -- plus the
@@ -16,8 +16,8 @@ import random
 
 import pytest
 
-from nanoserve_amd.block_manager import BlockAllocator, BlockSpaceManager, slots_for_range
-from nanoserve_amd.engine import SamplingParams, Sequence
+from nanoserve_amd.block_manager import BlockSpaceManager, slots_for_range
+from nanoserve_amd.scheduling import SamplingParams, Sequence
 from oracle.paged_attention import slot_mapping_ref
 
 
@@ -25,36 +25,46 @@ def _seq(seq_id=0, prompt_len=10):
     return Sequence(seq_id, list(range(prompt_len)), SamplingParams(max_new_tokens=5))
 
 
-def test_allocator_round_trip_and_counts():
-    a = BlockAllocator(8)
-    got = a.allocate(3)
-    assert len(got) == 3 and a.num_free == 5 and a.num_used == 3
-    a.free(got)
-    assert a.num_free == 8 and a.num_used == 0
+class _Owner:
+    def __init__(self, seq_id=0):
+        self.seq_id = seq_id
+        self.block_table: list[int] = []
 
 
-def test_allocator_failure_takes_nothing_and_double_free_raises():
-    a = BlockAllocator(2)
-    with pytest.raises(MemoryError):
-        a.allocate(3)
-    assert a.num_free == 2
-    b = a.allocate(2)
-    a.free(b)
+def test_allocation_round_trip_and_counts():
+    m = BlockSpaceManager(4, 8, watermark=0.0)
+    s = _Owner()
+    assert m.allocate(s, 12) and len(s.block_table) == 3 and m.num_free_blocks == 5
+    m.free(s)
+    assert m.num_free_blocks == 8 and s.block_table == []
+
+
+def test_short_pool_takes_nothing_and_double_free_raises():
+    m = BlockSpaceManager(4, 2, watermark=0.0)
+    s = _Owner()
+    assert not m.allocate(s, 12)
+    assert m.num_free_blocks == 2 and s.block_table == []
+    assert m.allocate(s, 8)
+    held = list(s.block_table)
+    m.free(s)
+    s.block_table = held
     with pytest.raises(ValueError):
-        a.free(b)
+        m.free(s)
     with pytest.raises(ValueError):
-        BlockAllocator(0)
+        BlockSpaceManager(16, 0)
 
 
 def test_blocks_are_never_handed_out_twice():
-    a = BlockAllocator(16)
-    x, y = a.allocate(5), a.allocate(5)
-    assert not set(x) & set(y)
-    a.free(x)
-    z = a.allocate(5)
-    assert not set(z) & set(y)
-    a.reset()
-    assert a.num_free == 16 and a.num_used == 0
+    m = BlockSpaceManager(1, 16, watermark=0.0)
+    x, y = _Owner(0), _Owner(1)
+    m.allocate(x, 5)
+    m.allocate(y, 5)
+    assert not set(x.block_table) & set(y.block_table)
+    m.free(x)
+    z = _Owner(2)
+    m.allocate(z, 5)
+    assert not set(z.block_table) & set(y.block_table)
+    assert sorted(set(z.block_table) | set(y.block_table)) == sorted(z.block_table + y.block_table)
 
 
 def test_blocks_for_rounds_up():
@@ -96,7 +106,6 @@ def test_free_returns_every_block():
     for s in seqs:
         m.free(s)
     assert m.num_free_blocks == 32 and all(s.block_table == [] for s in seqs)
-    assert m.utilization() == 0.0
 
 
 def test_slot_mapping_matches_the_closed_form():
@@ -164,12 +173,3 @@ def test_block_runs_equal_per_token_brute_force():
         end = rng.randint(0, len(table) * bs)
         start = rng.randint(0, end)
         assert slots_for_range(table, start, end, bs) == slot_mapping_ref(table, start, end, bs)
-
-
-def test_fragmentation_is_below_one_block_per_sequence():
-    m = BlockSpaceManager(16, 64)
-    seqs = [_seq(i, prompt_len=n) for i, n in enumerate((1, 16, 17, 40))]
-    for s in seqs:
-        m.allocate(s, s.num_tokens)
-    waste = m.fragmentation_waste(seqs)
-    assert waste == (16 - 1) + 0 + (32 - 17) + (48 - 40)

@@ -1,12 +1,10 @@
-"""The engine harness on the CPU: model oracle, scheduler and runner bookkeeping.
+"""The engine harness on the CPU: model oracle and runner bookkeeping.
 
 * The model oracle (oracle/qwen2.py) is pinned against an independent
   implementation: transformers' own Qwen2ForCausalLM on identical float32
   weights (the reference's third model property, reference
   tests/test_model.py:1-14), both for one-shot prefill and for incremental
   decode through the paged cache.
-* The scheduler follows the reference rules (scheduler.py:91-262): running
-  first, token budget, chunked prefill, newest-first preemption by recompute.
 * The runner's metadata is the engine layout (model_runner.py:85-147).
 """
 
@@ -16,8 +14,8 @@ import pytest
 import torch
 
 from nanoserve_amd.block_manager import BlockSpaceManager
-from nanoserve_amd.engine import (ModelRunner, RequestMetrics, SamplingParams, Scheduler, SchedulerConfig,
-                                  Sequence, SeqStatus, summarize)
+from nanoserve_amd.engine import ModelRunner, summarize
+from nanoserve_amd.scheduling import RequestMetrics, SamplingParams, Sequence
 from nanoserve_amd.metadata import ScheduledSeq, build_metadata
 from nanoserve_amd.model import Qwen2Config, Qwen2ForCausalLM, random_init_
 from oracle.qwen2 import qwen2_forward_ref, relative_error
@@ -81,95 +79,8 @@ def test_oracle_incremental_decode_matches_transformers():
         assert relative_error(got[0], want[t]) < 1e-4
 
 
-# ---- scheduler -------------------------------------------------------------
 def _seq(i, n_prompt, max_new=4):
     return Sequence(i, list(range(n_prompt)), SamplingParams(max_new_tokens=max_new, ignore_eos=True))
-
-
-def _sched(budget=64, max_seqs=8, blocks=64, bs=4, chunked=True):
-    bm = BlockSpaceManager(bs, blocks, watermark=0.0)
-    return Scheduler(SchedulerConfig(budget, max_seqs, chunked), bm), bm
-
-
-def _finish_step(out):
-    """What the runner and engine do after a step: advance, emit a token when due."""
-    for seq, q in out.scheduled:
-        seq.advance_computed(q)
-        if seq.num_computed_tokens == seq.num_tokens:
-            seq.output_token_ids.append(0)
-            seq.check_stop(None)
-
-
-def test_budget_is_shared_and_prompts_are_chunked():
-    s, _ = _sched(budget=10)
-    a, b = _seq(0, 7), _seq(1, 9)
-    s.add(a)
-    s.add(b)
-    out = s.schedule()
-    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 7), (1, 3)]
-    _finish_step(out)
-    out = s.schedule()
-    # a decodes first (running sequences get the budget first), b continues its prefill.
-    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 1), (1, 6)]
-
-
-def test_unchunked_prefill_waits_for_a_whole_budget():
-    s, _ = _sched(budget=10, chunked=False)
-    a, b = _seq(0, 7), _seq(1, 9)
-    s.add(a)
-    s.add(b)
-    out = s.schedule()
-    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 7)]
-    with pytest.raises(ValueError):
-        s2, _ = _sched(budget=8, chunked=False)
-        s2.add(_seq(2, 9))
-        s2.schedule()
-
-
-def test_max_num_seqs_caps_admission():
-    s, _ = _sched(budget=100, max_seqs=2)
-    for i in range(3):
-        s.add(_seq(i, 5))
-    out = s.schedule()
-    assert [x.seq_id for x, _ in out.scheduled] == [0, 1]
-    assert len(s.waiting) == 1
-
-
-def test_out_of_blocks_preempts_the_newest_and_recomputes():
-    # 6 blocks of 4 tokens: two 11-token prompts take 3 blocks each; the first
-    # decode step needs a 4th block for sequence 0 and evicts sequence 1.
-    s, bm = _sched(budget=64, blocks=6, bs=4)
-    a, b = _seq(0, 11, max_new=8), _seq(1, 11, max_new=8)
-    s.add(a)
-    s.add(b)
-    _finish_step(s.schedule())
-    assert bm.num_free_blocks == 0
-    _finish_step(s.schedule())  # both decode a 12th token: still 3 blocks each
-    out = s.schedule()          # position 12 needs a 4th block
-    assert [x.seq_id for x in out.preempted] == [1]
-    assert b.status is SeqStatus.PREEMPTED and b.num_computed_tokens == 0 and b.block_table == []
-    assert s.waiting[0] is b and b.num_preemptions == 1
-    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 1)]
-    # Recompute later covers prompt + generated tokens in one prefill.
-    assert b.num_uncomputed_tokens == 13
-
-
-def test_request_larger_than_the_cache_is_rejected():
-    s, _ = _sched(budget=64, blocks=2, bs=4)
-    s.add(_seq(0, 8, max_new=4))
-    _finish_step(s.schedule())
-    with pytest.raises(ValueError):
-        s.schedule()
-
-
-def test_finished_sequences_release_their_blocks():
-    s, bm = _sched(budget=64, blocks=16, bs=4)
-    a = _seq(0, 5, max_new=1)
-    s.add(a)
-    _finish_step(s.schedule())
-    assert a.status is SeqStatus.FINISHED_LENGTH
-    assert s.free_finished() == [a]
-    assert bm.num_free_blocks == 16 and not s.has_work
 
 
 # ---- runner metadata -------------------------------------------------------

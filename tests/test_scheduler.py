@@ -1,14 +1,13 @@
-"""Continuous-batching rules of nanoserve_amd.engine.Scheduler (CPU only).
+"""Continuous-batching rules of nanoserve_amd.scheduling (CPU only).
 
 Bookkeeping bugs in a scheduler show up as livelock, leaked blocks or wrong
 batches, never as a numerical error, so these run in milliseconds on the CPU
 with a stand-in for the runner.  They cover the behaviours the reference pins
 for its scheduler (reference tests/test_scheduler.py:49-286, scheduler.py:
-91-262): admission under the token budget and the sequence cap, chunked and
-unchunked prefill, running sequences first, block exhaustion, newest-first
-preemption by recompute to the front of the queue, the no-preemption mode
-failing loudly, requests too large for the cache, progress under heavy
-pressure, and the step statistics.
+91-262) that shape config 5's batches: admission under the token budget and
+the sequence cap, chunked and unchunked prefill, running sequences first,
+block exhaustion, newest-first eviction by recompute to the front of the
+queue, requests too large for the cache, and progress under heavy pressure.
 """
 
 from __future__ import annotations
@@ -16,27 +15,26 @@ from __future__ import annotations
 import pytest
 
 from nanoserve_amd.block_manager import BlockSpaceManager
-from nanoserve_amd.engine import SamplingParams, Scheduler, SchedulerConfig, Sequence, SeqStatus
+from nanoserve_amd.scheduling import SamplingParams, Scheduler, SchedulerConfig, Sequence, SeqState
 
 
-def make(blocks=64, bs=16, budget=1024, max_seqs=256, chunked=True, preemption="recompute"):
+def make(blocks=64, bs=16, budget=1024, max_seqs=256, chunked=True):
     bm = BlockSpaceManager(bs, blocks, watermark=0.0)
-    cfg = SchedulerConfig(max_num_batched_tokens=budget, max_num_seqs=max_seqs,
-                          enable_chunked_prefill=chunked, preemption_mode=preemption)
+    cfg = SchedulerConfig(max_num_batched_tokens=budget, max_num_seqs=max_seqs, enable_chunked_prefill=chunked)
     return Scheduler(cfg, bm), bm
 
 
 def req(i, prompt, max_new=8):
-    return Sequence(i, [7] * prompt, SamplingParams(max_new_tokens=max_new, ignore_eos=True))
+    return Sequence(i, list(range(prompt)), SamplingParams(max_new_tokens=max_new, ignore_eos=True))
 
 
 def step(s, out):
     """The runner's and engine's part of a step: KV computed, a token when due, stops, frees."""
     for seq, q in out.scheduled:
-        seq.advance_computed(q)
+        seq.mark_computed(q)
         if seq.num_computed_tokens == seq.num_tokens:
             seq.output_token_ids.append(1)
-            seq.check_stop(None)
+            seq.check_done(None)
     return s.free_finished()
 
 
@@ -68,6 +66,19 @@ def test_prefill_then_decode_steps():
     assert (out.num_prefill_seqs, out.num_decode_seqs) == (0, 1)
 
 
+def test_budget_is_shared_and_prompts_are_chunked():
+    s, _ = make(budget=10, bs=4)
+    a, b = req(0, 7), req(1, 9)
+    s.add(a)
+    s.add(b)
+    out = s.schedule()
+    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 7), (1, 3)]
+    step(s, out)
+    out = s.schedule()
+    # a decodes first (running sequences get the budget first), b continues its prefill.
+    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 1), (1, 6)]
+
+
 def test_step_never_exceeds_the_token_budget():
     s, _ = make(budget=100)
     for i in range(5):
@@ -94,7 +105,7 @@ def test_everything_finishes_and_every_block_returns():
         s.add(req(i, 20, max_new=5))
     done = drain(s)
     assert sorted(x.seq_id for x in done) == list(range(6))
-    assert all(len(x.output_token_ids) == 5 and x.status is SeqStatus.FINISHED_LENGTH for x in done)
+    assert all(len(x.output_token_ids) == 5 and x.state is SeqState.DONE_LENGTH for x in done)
     assert bm.num_free_blocks == 128 and not s.has_work
 
 
@@ -105,7 +116,7 @@ def test_a_long_prompt_is_prefilled_in_budget_sized_chunks():
     while True:
         out = s.schedule()
         seq, q = out.scheduled[0]
-        if not seq.is_prefilling:
+        if not seq.in_prompt:
             break
         chunks.append(q)
         step(s, out)
@@ -120,7 +131,6 @@ def test_a_big_prompt_does_not_stall_running_decodes():
     out = s.schedule()
     assert (out.num_decode_seqs, out.num_prefill_seqs) == (1, 1)
     assert out.scheduled[0] == (s.running[0], 1) and out.num_batched_tokens == 64
-    assert s.stats.mixed_steps == 1
 
 
 def test_without_chunking_a_prompt_is_scheduled_whole_or_not_at_all():
@@ -147,64 +157,67 @@ def test_admission_stops_when_the_blocks_run_out():
     assert bm.num_free_blocks == 0 and len(s.waiting) == 8
 
 
-def _fill_and_grow(s, extra=None):
-    """Two 32-token prompts fill 4 blocks; decoding then needs a fifth."""
+def test_admission_keeps_the_watermark_but_growth_may_use_it():
+    bm = BlockSpaceManager(4, 10, watermark=0.2)
+    s = Scheduler(SchedulerConfig(max_num_batched_tokens=1000, max_num_seqs=8), bm)
+    s.add(req(0, 32, max_new=40))  # 8 blocks: exactly what admission may take
+    s.add(req(1, 4))
+    out = s.schedule()
+    assert [x.seq_id for x, _ in out.scheduled] == [0] and bm.num_free_blocks == 2
+    for _ in range(8):  # decoding fills the reserve
+        step(s, out)
+        out = s.schedule()
+    assert bm.num_free_blocks < 2 and not out.preempted
+
+
+def test_out_of_blocks_evicts_the_newest_and_recomputes():
+    # 6 blocks of 4 tokens: two 11-token prompts take 3 blocks each; the first
+    # decode step needs a 4th block for sequence 0 and evicts sequence 1.
+    s, bm = make(budget=64, blocks=6, bs=4)
+    a, b = req(0, 11, max_new=8), req(1, 11, max_new=8)
+    s.add(a)
+    s.add(b)
+    step(s, s.schedule())
+    assert bm.num_free_blocks == 0
+    step(s, s.schedule())  # both decode a 12th token: still 3 blocks each
+    out = s.schedule()     # position 12 needs a 4th block
+    assert [x.seq_id for x in out.preempted] == [1] and s.num_preemptions == 1
+    assert b.state is SeqState.EVICTED and b.num_computed_tokens == 0 and b.block_table == []
+    assert s.waiting[0] is b and b.num_evictions == 1
+    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 1)]
+    # Its generated tokens stay; the recompute prefills prompt and outputs together.
+    assert b.pending_tokens == 13 and b.token_slice(10, 13) == [10, 1, 1]
+
+
+def test_an_evicted_request_goes_to_the_front_of_the_queue():
+    s, _ = make(blocks=4, budget=10_000)
     for i in range(2):
         s.add(req(i, 32, max_new=200))
     step(s, s.schedule())
-    if extra is not None:
-        s.add(extra)
+    newcomer = req(99, 16, max_new=4)
+    s.add(newcomer)
     for _ in range(60):
         out = s.schedule()
         if out.preempted:
-            return out
+            break
         step(s, out)
-    raise AssertionError("no preemption happened")
-
-
-def test_growth_past_the_cache_preempts_the_newest_by_recompute():
-    s, bm = make(blocks=4, budget=10_000)
-    out = _fill_and_grow(s)
-    victim = out.preempted[0]
-    assert victim.seq_id == 1 and s.stats.total_preemptions == 1 == s.num_preemptions
-    assert victim.status is SeqStatus.PREEMPTED and victim.block_table == [] and victim.num_computed_tokens == 0
-    # Its generated tokens stay; the recompute prefills prompt and outputs together.
-    assert victim.output_token_ids and victim.num_uncomputed_tokens == 32 + len(victim.output_token_ids)
-    assert [(x.seq_id, q) for x, q in out.scheduled] == [(0, 1)]
-
-
-def test_a_preempted_request_goes_to_the_front_of_the_queue():
-    s, _ = make(blocks=4, budget=10_000)
-    newcomer = req(99, 16, max_new=4)
-    out = _fill_and_grow(s, extra=newcomer)
-    assert s.waiting[0] is out.preempted[0] and newcomer in s.waiting
-
-
-def test_without_preemption_exhaustion_raises_instead_of_stalling():
-    s, _ = make(blocks=4, budget=10_000, preemption="none")
-    for i in range(2):
-        s.add(req(i, 32, max_new=200))
-    with pytest.raises(RuntimeError, match="preemption disabled"):
-        drain(s, limit=60)
-    with pytest.raises(ValueError):
-        Scheduler(SchedulerConfig(preemption_mode="swap"), BlockSpaceManager(16, 4, watermark=0.0))
+    assert out.preempted and s.waiting[0] is out.preempted[0] and newcomer in s.waiting
 
 
 def test_a_request_larger_than_the_cache_is_rejected():
-    for mode in ("recompute", "none"):
-        s, _ = make(blocks=2, budget=10_000, preemption=mode)
-        s.add(req(0, 16, max_new=200))
-        with pytest.raises(ValueError, match="KV blocks"):
-            drain(s, limit=400)
+    s, _ = make(blocks=2, budget=10_000)
+    s.add(req(0, 16, max_new=200))
+    with pytest.raises(ValueError, match="cannot fit the KV cache"):
+        drain(s, limit=400)
 
 
-def test_the_queue_drains_under_constant_preemption():
+def test_the_queue_drains_under_constant_eviction():
     s, bm = make(blocks=12, budget=512)
     for i in range(8):
         s.add(req(i, 48, max_new=24))
     done = drain(s)
     assert len(done) == 8 and all(len(x.output_token_ids) == 24 for x in done)
-    assert s.stats.total_preemptions > 0 and bm.num_free_blocks == 12
+    assert s.num_preemptions > 0 and bm.num_free_blocks == 12
 
 
 def test_running_sequences_are_served_before_new_ones():
@@ -216,12 +229,18 @@ def test_running_sequences_are_served_before_new_ones():
     assert out.scheduled[0][0].seq_id == 0 and out.scheduled[0][1] == 1
 
 
-def test_statistics_count_every_token():
-    s, _ = make(blocks=256)
-    for i in range(4):
-        s.add(req(i, 32, max_new=6))
-    drain(s)
-    st = s.stats
-    assert st.total_prefill_tokens == 4 * 32
-    assert st.total_decode_tokens == 4 * 5  # the last token is sampled, never fed back
-    assert st.total_steps == 6 and st.mean_batch_size == 4.0 and st.total_preemptions == 0
+def test_finished_sequences_release_their_blocks():
+    s, bm = make(budget=64, blocks=16, bs=4)
+    a = req(0, 5, max_new=1)
+    s.add(a)
+    step(s, s.schedule())
+    assert a.state is SeqState.DONE_LENGTH and bm.num_free_blocks == 16 and not s.has_work
+
+
+def test_eos_stops_unless_ignored():
+    a = Sequence(0, [1, 2], SamplingParams(max_new_tokens=5))
+    a.output_token_ids.append(7)
+    assert a.check_done(7) and a.state is SeqState.DONE_EOS
+    b = Sequence(1, [1, 2], SamplingParams(max_new_tokens=5, ignore_eos=True))
+    b.output_token_ids.append(7)
+    assert not b.check_done(7) and b.state is SeqState.QUEUED
