@@ -2,36 +2,41 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2]
 
-A step is one call of the paged-attention op on one batch (config c2 by
-default: decode, B=32, Qwen2.5-0.5B heads 14/2/64, block 16, fp16, lognormal
-contexts).  Inputs are resident in HBM before timing.
+A step is one serving step's worth of the paged-attention op: the engine
+builds one AttentionMetadata (block tables, lengths) per step and every layer
+of the model calls attention with it on that layer's own K/V cache and
+queries (reference qwen2.py:105-113, model_runner.py:85-168).  So a step here
+is --layers (24, Qwen2.5-0.5B) calls on one batch (config c2 by default:
+decode, B=32, Qwen2.5-0.5B heads 14/2/64, block 16, fp16, lognormal
+contexts), each with its own freshly drawn caches and queries.  The benchmark
+holds several distinct steps (different seeds, i.e. different length draws
+and block tables), enough that their caches together exceed 1.2 GB, so K/V
+are always read from HBM and not from the 256 MB Infinity Cache.  Inputs are
+resident in HBM before timing.
 
-The calls are laid out the way the engine issues them: a serving step builds
-one AttentionMetadata (block tables, lengths) and every layer of the model
-calls attention with it on that layer's own K/V cache and queries
-(reference qwen2.py:105-113, model_runner.py:85-168).  So the benchmark holds
-several steps (different seeds, i.e. different length draws and block
-tables) of --layers calls each, every call with its own freshly drawn caches
-and queries; the caches of all calls together exceed 1.2 GB, so KV is always
-read from HBM and not from the 256 MB Infinity Cache.  A second pass gives
-every call its own metadata too (nothing shared, every table read cold) and is
-reported as `cold_metadata`.
-
-The K timed calls are replayed from a HIP graph captured over the calls (a
-serving loop issues them the same way), bracketed by device synchronisation,
-and timed with HIP events on the launch stream.  A decode batch is one kernel
-launch, so us per call is us per launch.
+Exactly K steps are timed: they are replayed from HIP graphs captured over
+the steps (a serving loop issues them the same way), cycling the distinct
+steps, bracketed by device synchronisation and timed with HIP events on the
+launch stream.  --cold adds a pass in which every call has its own metadata
+too (nothing shared, every table read cold).
 
 Prints one JSON line: value = algorithmic KV GB/s (sum_i 2*L_i*Hkv*D*itemsize
-per call / time per call), plus us/call, % of the 8 TB/s HBM peak, the
-reshape_and_cache time for the batch's new tokens, and a CPU baseline: the
-repo's torch gather+SDPA oracle timed on this host on a bounded sample.
+per call, summed over the timed calls / time), plus us per call, % of the
+8 TB/s HBM peak, the reshape_and_cache time for the batch's new tokens, and a
+CPU baseline: the repo's torch gather+SDPA oracle timed on this host on a
+bounded sample.
+
+Other modes: --config c5 runs the engine benchmark (config 5), --floors the
+launch and streaming-read floors, --ref-grid the reference's own grid of
+uniform-context decode shapes, --copy-calibration the known-size copy that
+scales rocprofv3 byte counters.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -57,8 +62,8 @@ C5_METRIC = "engine output tok/s + p99 TPOT, Qwen2.5-0.5B INT4 g128, 32 lognorma
 def parse_args(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
-    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--steps", type=int, default=200, help="serving steps timed (each --layers calls)")
+    ap.add_argument("--warmup", type=int, default=20, help="serving steps replayed before timing")
     ap.add_argument("--config", default="c2", choices=sorted(WORKLOADS))
     ap.add_argument("--block-size", type=int, default=None)
     ap.add_argument("--seed", type=int, default=0)
@@ -67,25 +72,19 @@ def parse_args(argv=None):
     ap.add_argument("--min-steps", type=int, default=4, help="distinct serving steps (length draws)")
     ap.add_argument("--replica-gb", type=float, default=1.2,
                     help="minimum combined K/V footprint of the calls cycled through")
-    ap.add_argument("--no-cold", action="store_true", help="skip the all-cold-metadata pass")
+    ap.add_argument("--cold", action="store_true",
+                    help="also time steps whose calls each have their own metadata (cold metadata)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-calls", type=int, default=20)
     ap.add_argument("--eager", action="store_true", help="also time K eager (non-graph) calls")
+    ap.add_argument("--floors", action="store_true",
+                    help="only time an empty launch and streaming reads of c2's byte counts and exit")
+    ap.add_argument("--ref-grid", action="store_true",
+                    help="only run the reference's B x uniform-ctx grid (with its correctness gate) and exit")
     ap.add_argument("--copy-calibration", type=float, default=None, metavar="MB",
                     help="only run 5 plain device copies of MB megabytes (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings) and exit")
     return ap.parse_args(argv)
-
-
-def _c5_requests(n, seed, vocab):
-    """Prompt/output lengths by the reference's lognormal rule (workload.py:57-75), random token ids."""
-    import numpy as np
-
-    rng = np.random.default_rng(seed)
-    p_lens = np.clip(rng.lognormal(np.log(256), 0.7, n).astype(int), 16, 2048)
-    o_lens = np.clip(rng.lognormal(np.log(128), 0.7, n).astype(int), 8, 1024)
-    tok = np.random.default_rng(seed + 1)
-    return [(tok.integers(0, vocab, int(p)).tolist(), int(o)) for p, o in zip(p_lens, o_lens)]
 
 
 def _bench_engine(torch, args):
@@ -93,6 +92,7 @@ def _bench_engine(torch, args):
     from nanoserve_amd.engine import LLMEngine, SamplingParams, SchedulerConfig, summarize
     from nanoserve_amd.model import Qwen2Config, Qwen2ForCausalLM, random_init_
     from nanoserve_amd.quant import quantize_model
+    from nanoserve_amd.workloads import c5_requests
 
     cfg = Qwen2Config()
     model = random_init_(Qwen2ForCausalLM(cfg, max_position=4096), std=0.02, seed=args.seed)
@@ -101,7 +101,7 @@ def _bench_engine(torch, args):
     model.fuse_projections()
     block_size = args.block_size or 16
 
-    reqs = _c5_requests(32, args.seed, cfg.vocab_size)
+    reqs = c5_requests(32, args.seed, cfg.vocab_size)
 
     def run(use_graphs):
         eng = LLMEngine(model, num_blocks=8192, block_size=block_size, device="cuda",
@@ -110,7 +110,7 @@ def _bench_engine(torch, args):
         if use_graphs:
             eng.runner.graphs.capture_all()  # capture is set-up, not serving time
         # Warm-up: a short run of the same shape mix (kernels, allocator, workspaces).
-        for toks, n in _c5_requests(8, args.seed + 7, cfg.vocab_size):
+        for toks, n in c5_requests(8, args.seed + 7, cfg.vocab_size):
             eng.add_request(toks[:64], SamplingParams(max_new_tokens=min(n, 16), ignore_eos=True))
         eng.run_all()
         eng.finished.clear()
@@ -173,10 +173,138 @@ def _copy_calibration(torch, mb):
     return 0
 
 
+def _graph_time(torch, stream, launch, n, reps=3):
+    """Seconds per launch of `launch(i)` for i in [0, n), captured in one HIP
+    graph and replayed (best of `reps` timed replays after one warm replay)."""
+    with torch.cuda.stream(stream):
+        for i in range(n):
+            launch(i)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for i in range(n):
+            launch(i)
+    best = float("inf")
+    with torch.cuda.stream(stream):
+        g.replay()
+        stream.synchronize()
+        for _ in range(reps):
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            g.replay()
+            end.record(stream)
+            end.synchronize()
+            best = min(best, start.elapsed_time(end) * 1e-3 / n)
+    return best
+
+
+def _floors(torch, args):
+    """What any kernel pays on this device, graph-replayed back to back: an empty
+    launch, and one streaming read of N bytes from HBM (each launch reads its own
+    slice of a pool larger than the 256 MB MALL), for c2's byte counts and a
+    large read.  ns_stream_read (csrc/floors.hip) is the kernel for both."""
+    from nanoserve_amd import _lib
+
+    lib = _lib.load()
+    stream = torch.cuda.Stream()
+    sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
+    pool_bytes = int(args.replica_gb * 1e9) // 4096 * 4096
+    pool = torch.randint(0, 255, (pool_bytes,), dtype=torch.uint8, device="cuda")
+    rows = []
+    for grid in (256, 512, 1024):
+        t = _graph_time(torch, stream, lambda i: _lib.check(
+            lib.ns_stream_read(None, 0, sink.data_ptr(), grid, stream.cuda_stream), "ns_stream_read"), 200)
+        rows.append({"what": "empty launch", "grid": grid, "us_per_launch": round(t * 1e6, 3)})
+    c2_seed0, c2_mean = 18_071_552, 21_328_640  # algorithmic K/V bytes of the c2 calls (seed 0; four seeds)
+    for nbytes in (c2_seed0, c2_mean, 64 << 20, 1 << 30):
+        nbytes = nbytes // 16 * 16
+        per = max(1, min(pool_bytes // nbytes, 200))
+        best = None
+        for grid in (256, 512, 1024, 2048, 4096):
+            def launch(i, nbytes=nbytes, grid=grid):
+                src = pool.data_ptr() + (i % per) * nbytes
+                _lib.check(lib.ns_stream_read(src, nbytes, sink.data_ptr(), grid, stream.cuda_stream),
+                           "ns_stream_read")
+            t = _graph_time(torch, stream, launch, per if nbytes < (256 << 20) else 2)
+            if best is None or t < best[1]:
+                best = (grid, t)
+        grid, t = best
+        rows.append({"what": "streaming read", "bytes": nbytes, "best_grid": grid,
+                     "us_per_launch": round(t * 1e6, 3), "gbs": round(nbytes / t / 1e9, 1),
+                     "frac_of_hbm_peak": round(nbytes / t / 1e9 / HBM_PEAK_GBS, 4)})
+    print(json.dumps({"floors": rows, "device": torch.cuda.get_device_name(0),
+                      "timing": "HIP-graph replay of back-to-back launches, hipEvents, best of 3"}))
+    return 0
+
+
+def _uniform_case(torch, batch, ctx, dev):
+    """The reference's grid case (bench/bench_attention.py:83-121): `batch`
+    sequences of exactly `ctx` tokens, Hq14/Hkv2/D64, block 16, fp16, caches of
+    exactly the blocks needed, block tables a seeded random permutation (int32)."""
+    from nanoserve_amd.workloads import PagedCase, metadata_for
+
+    bs, hq, hkv, d = 16, 14, 2, 64
+    per = -(-ctx // bs)
+    nb = batch * per
+    g = torch.Generator().manual_seed(0)
+    kc = torch.randn(nb, bs, hkv, d, generator=g).half().to(dev)
+    vc = torch.randn(nb, bs, hkv, d, generator=g).half().to(dev)
+    perm = torch.randperm(nb, generator=g).tolist()
+    tables = [perm[i * per:(i + 1) * per] for i in range(batch)]
+    q = torch.randn(batch, hq, d, generator=g).half().to(dev)
+    md = metadata_for([ctx] * batch, [1] * batch, tables, bs, dev, index_dtype=torch.int32)
+    return PagedCase("grid", 0, q, kc, vc, md, 1.0 / math.sqrt(d), [ctx] * batch, [1] * batch, tables)
+
+
+def _ref_grid(torch, args):
+    """The reference's measurement grid on this GPU: B in {1, 8, 32} x uniform
+    ctx in {128, 512, 1024, 2048, 4096}, with its correctness gate before timing
+    (reference bench/bench_attention.py:124-240).  Like the reference, each
+    case's caches are reused by every timed call (so small cases run from the
+    MALL); times are HIP-graph replays of 50 calls and eager calls through the
+    Python shim, after 10 warm-up calls."""
+    from nanoserve_amd import paged_attention_hip
+
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.Stream()
+    rows = []
+    for batch in (1, 8, 32):
+        for ctx in (128, 512, 1024, 2048, 4096):
+            case = _uniform_case(torch, batch, ctx, dev)
+            out = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
+            err = _oracle_err(case, out)
+            row = {"batch": batch, "ctx": ctx, "max_abs_err_vs_oracle": err}
+            if not err <= 2e-3:
+                row["status"] = "MISMATCH"
+                rows.append(row)
+                continue
+            call = lambda i: paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
+            t_graph = _graph_time(torch, stream, call, 50)
+            with torch.cuda.stream(stream):
+                for i in range(10):
+                    call(i)
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                for i in range(50):
+                    call(i)
+                end.record(stream)
+            end.synchronize()
+            t_eager = start.elapsed_time(end) * 1e-3 / 50
+            kv = 2 * batch * ctx * 2 * 64 * 2  # bench_attention.py:178-180
+            row.update({"kv_bytes": kv, "graph_us": round(t_graph * 1e6, 3), "eager_us": round(t_eager * 1e6, 3),
+                        "graph_gbs": round(kv / t_graph / 1e9, 1), "eager_gbs": round(kv / t_eager / 1e9, 1)})
+            rows.append(row)
+            print(json.dumps(row), flush=True)
+            del case
+    print(json.dumps({"ref_grid": rows, "device": torch.cuda.get_device_name(0)}))
+    return 1 if any(r.get("status") == "MISMATCH" for r in rows) else 0
+
+
 def _profiled_traffic(args):
     """HBM bytes per launch measured with rocprofv3 FETCH_SIZE + WRITE_SIZE for
     this exact workload (profiles/paged_decode_<config>_traffic.md), or None."""
-    if args.seed != 0 or args.block_size is not None or args.layers != 24 or args.min_steps != 4:
+    if (args.seed != 0 or args.block_size is not None or args.layers != 24 or args.min_steps != 4
+            or args.steps % args.min_steps):
         return None, None
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                         f"paged_decode_{args.config}_traffic.md")
@@ -264,21 +392,30 @@ def _oracle_err(case_gpu, gpu_out):
     return (gpu_out.float().cpu() - ref).abs().max().item()
 
 
-def _build_calls(args, dev, shared):
-    """Calls to cycle through: steps of --layers calls sharing one metadata
-    (shared=True) or fully independent calls (shared=False)."""
+def _build_steps(args, dev, shared):
+    """Serving steps to cycle through.  With shared=True a step is --layers
+    attention calls that share one metadata (lengths, block tables) but each
+    have their own K/V caches, as the layers of one engine step do
+    (reference qwen2.py:105-113); with shared=False every call of the step has
+    its own metadata too.  Steps are added until their combined K/V footprint
+    exceeds --replica-gb (so K/V come from HBM, not the 256 MB MALL) and
+    there are at least --min-steps of them."""
     from nanoserve_amd.workloads import make_case, make_layer
 
-    calls, total, step = [], 0, 0
-    while total < args.replica_gb * 1e9 or step < (args.min_steps if shared else 2):
-        base = make_case(args.config, seed=args.seed + step, device=dev, gen_device=dev,
-                         block_size=args.block_size)
-        for layer in range(args.layers if shared else 1):
-            c = base if layer == 0 else make_layer(base, seed=1000 * (args.seed + step) + layer, gen_device=dev)
+    steps, total, j = [], 0, 0
+    while total < args.replica_gb * 1e9 or j < args.min_steps:
+        calls = []
+        for layer in range(args.layers):
+            if layer == 0 or not shared:
+                seed = args.seed + j if layer == 0 else 10_000 + 1000 * (args.seed + j) + layer
+                c = make_case(args.config, seed=seed, device=dev, gen_device=dev, block_size=args.block_size)
+            else:
+                c = make_layer(calls[0], seed=1000 * (args.seed + j) + layer, gen_device=dev)
             calls.append(c)
             total += _kv_footprint(c)
-        step += 1
-    return calls, total, step
+        steps.append(calls)
+        j += 1
+    return steps, total
 
 
 def _rope_inputs(torch, calls, news):
@@ -307,11 +444,17 @@ def _rope_bytes(c) -> int:
     return T * (2 * (Hq + 2 * c.num_kv_heads) * D + 2 * D) * c.query.element_size()
 
 
-def _time_calls(torch, calls, news, K, warmup, stream):
-    """Warm up, capture all calls in one HIP graph, time K replayed calls."""
+def _time_steps(torch, steps, news, K, warmup, stream):
+    """Warm up, capture the serving steps in one HIP graph, time exactly K steps.
+
+    Step k of the timed sequence is steps[k % R] (R = len(steps)): the graph of
+    all R steps is replayed K // R times, then a graph of the first K % R
+    steps once, so the timed calls are exactly K * calls-per-step calls and
+    their bytes are summed exactly."""
     from nanoserve_amd import paged_attention_hip, reshape_and_cache, rope_reshape_and_cache
 
-    R = len(calls)
+    calls = [c for st in steps for c in st]
+    R, L = len(steps), len(steps[0])
 
     def attn(i):
         c = calls[i]
@@ -321,36 +464,39 @@ def _time_calls(torch, calls, news, K, warmup, stream):
         c = calls[i]
         reshape_and_cache(news[i][0], news[i][1], c.k_cache, c.v_cache, c.md.slot_mapping)
 
+    def run_steps(n, keep=None):
+        for j in range(n):
+            for i in range(j * L, (j + 1) * L):
+                out = attn(i)
+                if keep is not None:
+                    keep[i] = out  # graph-owned: holds the latest replay's result
+
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         # Write-then-attend, as the model's call site does (reference
         # qwen2.py:57-65): every call's new-token K/V goes in first.  Rewriting
         # the same rows later leaves the caches unchanged.
-        for i in range(R):
+        for i in range(len(calls)):
             write(i)
         first_out = attn(0).clone()
-        for w in range(max(warmup, R)):
-            attn(w % R)
+        run_steps(R)
     torch.cuda.synchronize()
 
-    def capture(fn, idxs, keep=None):
+    def capture(fn):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=stream):
-            for i in idxs:
-                out = fn(i)
-                if keep is not None:
-                    keep[i] = out  # graph-owned: holds the latest replay's result
+            fn()
         return g
 
     full, rem = divmod(K, R)
     replay_outs = {}
-    g_attn = capture(attn, range(R), replay_outs)
-    g_rem = capture(attn, range(rem)) if rem else None
-    g_write = capture(write, range(R))
+    g_all = capture(lambda: run_steps(R, replay_outs))
+    g_rem = capture(lambda: run_steps(rem)) if rem else None
+    g_write = capture(lambda: [write(i) for i in range(len(calls))])
 
-    def timed(graph, graph_rem, reps):
+    def timed(graph, reps, graph_rem=None, warm=1):
         with torch.cuda.stream(stream):
-            for _ in range(2):
+            for _ in range(warm):
                 graph.replay()
             stream.synchronize()
             start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -363,14 +509,15 @@ def _time_calls(torch, calls, news, K, warmup, stream):
         end.synchronize()
         return start.elapsed_time(end) * 1e-3
 
+    warm_reps = max(1, -(-warmup // R))
     # Timed twice (the reference's run-twice check, diagnose.py:241-263); the
     # line reports the mean and flags a spread over 15%.
-    t_runs = [timed(g_attn, g_rem, full), timed(g_attn, g_rem, full)]
+    t_runs = [timed(g_all, full, g_rem, warm_reps), timed(g_all, full, g_rem, 1)]
     t_attn = sum(t_runs) / 2
+    n_calls = K * L
     kv = [c.kv_bytes() for c in calls]
-    bytes_total = full * sum(kv) + sum(kv[:rem])
-    write_reps = max(1, K // R)
-    t_write = timed(g_write, None, write_reps)
+    bytes_total = full * sum(kv) + sum(kv[:rem * L])
+    t_write = timed(g_write, 1)
 
     # Fused rotary + cache write of the same new tokens (q rotated into a
     # separate buffer so the timed attention inputs stay as they are).
@@ -384,32 +531,36 @@ def _time_calls(torch, calls, news, K, warmup, stream):
                                c.md.slot_mapping, out=q_out)
 
     with torch.cuda.stream(stream):
-        for i in range(R):
+        for i in range(len(calls)):
             rope(i)
     stream.synchronize()
-    g_rope = capture(rope, range(R))
-    t_rope = timed(g_rope, None, write_reps)
+    g_rope = capture(lambda: [rope(i) for i in range(len(calls))])
+    t_rope = timed(g_rope, 1)
     with torch.cuda.stream(stream):
         g_write.replay()
     stream.synchronize()
-    rope_bytes = sum(_rope_bytes(c) for c in calls) / R
+    rope_bytes = sum(_rope_bytes(c) for c in calls) / len(calls)
     # The timed replays cycled every call's data through the same split-K
     # workspace: check a few replayed outputs against the oracle.
-    g_attn.replay()
+    g_all.replay()
     stream.synchronize()
-    checked = sorted({0, 1, R // 2, R - 1})
+    checked = sorted({0, 1, len(calls) // 2, len(calls) - 1})
     replay_err = max(_oracle_err(calls[i], replay_outs[i]) for i in checked)
-    del g_attn, g_rem, g_write, g_rope, rope_in
+    timed_steps = [steps[k % R] for k in range(min(K, R))]
+    del g_all, g_rem, g_write, g_rope, rope_in
     return {
         "replay_err": replay_err,
         "replay_checked": checked,
-        "s_per_call": t_attn / K,
-        "runs_us_per_call": [t / K * 1e6 for t in t_runs],
+        "s_per_call": t_attn / n_calls,
+        "s_per_step": t_attn / K,
+        "runs_us_per_call": [t / n_calls * 1e6 for t in t_runs],
         "gbs": bytes_total / t_attn / 1e9,
-        "write_us": t_write / (write_reps * R) * 1e6,
-        "rope_us": t_rope / (write_reps * R) * 1e6,
+        "write_us": t_write / len(calls) * 1e6,
+        "rope_us": t_rope / len(calls) * 1e6,
         "rope_bytes": rope_bytes,
-        "kv_mean": sum(kv) / R,
+        "kv_mean_timed": bytes_total / n_calls,
+        "calls_timed": n_calls,
+        "seeds_timed": sorted({st[0].seed for st in timed_steps}),
         "first_out": first_out,
         "attn": attn,
     }
@@ -431,6 +582,10 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     if args.copy_calibration is not None:
         return _copy_calibration(torch, args.copy_calibration)
+    if args.floors:
+        return _floors(torch, args)
+    if args.ref_grid:
+        return _ref_grid(torch, args)
     if args.config == "c5":
         return _bench_engine(torch, args)
     stream = torch.cuda.Stream(dev)
@@ -445,10 +600,11 @@ def main(argv=None):
         return out
 
     K = args.steps
-    calls, total, nsteps = _build_calls(args, dev, shared=True)
+    steps, total = _build_steps(args, dev, shared=True)
+    calls = [c for st in steps for c in st]
     dtype = calls[0].query.dtype
     dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
-    res = _time_calls(torch, calls, new_tokens(calls), K, args.warmup, stream)
+    res = _time_steps(torch, steps, new_tokens(calls), K, args.warmup, stream)
 
     eager_us = None
     if args.eager:
@@ -456,10 +612,10 @@ def main(argv=None):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         with torch.cuda.stream(stream):
-            for k in range(K):
+            for k in range(K * args.layers):
                 attn(k % len(calls))
         torch.cuda.synchronize()
-        eager_us = (time.perf_counter() - t0) / K * 1e6
+        eager_us = (time.perf_counter() - t0) / (K * args.layers) * 1e6
 
     gbs, s_per_call = res["gbs"], res["s_per_call"]
     traffic, traffic_src = _profiled_traffic(args)
@@ -470,7 +626,7 @@ def main(argv=None):
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": s_per_call * 1e3,
+        "ms_per_step": res["s_per_step"] * 1e3,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -478,16 +634,19 @@ def main(argv=None):
         "data": "synthetic",
         "config": {
             "workload": f"{args.config}: {WORKLOADS[args.config]}",
+            "step": f"one serving step: {args.layers} attention calls (one per layer) sharing the step's "
+                    "metadata, each over its own K/V caches",
             "block_size": calls[0].k_cache.shape[1],
             "global_batch": calls[0].md.num_seqs,
             "tokens_per_call": calls[0].md.num_tokens,
-            "serving_steps": nsteps,
             "layers_per_step": args.layers,
-            "calls_cycled": len(calls),
+            "distinct_steps": len(steps),
             "kv_footprint_gb": round(total / 1e9, 3),
-            "seeds": f"{args.seed}..{args.seed + nsteps - 1}",
-            "kv_bytes_per_call_mean": res["kv_mean"],
-            "timing": "HIP-graph replay of K calls cycling all steps x layers, hipEvents on the launch stream",
+            "calls_timed": res["calls_timed"],
+            "seeds_timed": res["seeds_timed"],
+            "kv_bytes_per_call_mean": res["kv_mean_timed"],
+            "timing": "HIP-graph replay of exactly K serving steps cycling the distinct steps, "
+                      "hipEvents on the launch stream",
         },
         "us_per_call": round(s_per_call * 1e6, 3),
         "timed_runs_us_per_call": [round(x, 3) for x in res["runs_us_per_call"]],
@@ -525,18 +684,18 @@ def main(argv=None):
     first_case, first_out = calls[0], res["first_out"]
     del res
 
-    if not args.no_cold:
-        del calls
-        cold_args = argparse.Namespace(**vars(args))
-        cold, _, _ = _build_calls(cold_args, dev, shared=False)
-        r2 = _time_calls(torch, cold, new_tokens(cold), K, args.warmup, stream)
+    if args.cold:
+        del calls, steps
+        cold, _ = _build_steps(args, dev, shared=False)
+        cold_calls = [c for st in cold for c in st]
+        r2 = _time_steps(torch, cold, new_tokens(cold_calls), K, args.warmup, stream)
         result["cold_metadata"] = {
             "us_per_call": round(r2["s_per_call"] * 1e6, 3),
             "gbs": round(r2["gbs"], 2),
-            "calls_cycled": len(cold),
+            "calls_timed": r2["calls_timed"],
             "note": "every call with its own block tables and lengths (no step shares metadata)",
         }
-        del cold, r2
+        del cold, cold_calls, r2
 
     if not args.no_cpu_baseline:
         cpu, err = _cpu_baseline(first_case, args.cpu_calls, first_out)

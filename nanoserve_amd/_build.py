@@ -23,7 +23,7 @@ INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libnanoserve_paged.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["paged_attention.hip", "reshape_and_cache.hip", "rope_cache.hip", "int4_linear.hip",
-           "argmax.hip"]
+           "argmax.hip", "floors.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [

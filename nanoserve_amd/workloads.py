@@ -12,6 +12,9 @@ Each config describes one attention call over a paged cache:
       inside the chunk, flattened without padding (T = 2076).
   c4  larger-GQA long-context decode, B=64, Hq28/Hkv4/D128, bf16, context
       lognormal(median 4096, sigma 1.0) clipped to [128, 32768], block 16 or 32.
+  c5  the engine's request mix (c5_requests): 32 requests, prompt lengths
+      lognormal(median 256, sigma 0.7) clipped to [16, 2048], output lengths
+      lognormal(median 128, sigma 0.7) clipped to [8, 1024], random token ids.
 
 Lengths use numpy's lognormal with mu = log(median) truncated to int then
 clipped, the convention of the reference workload generator
@@ -209,3 +212,13 @@ def metadata_for(seq_lens: list[int], query_lens: list[int], tables: list[list[i
         seq_lens_cpu=list(seq_lens),
         query_start_loc_cpu=qsl,
     )
+
+
+def c5_requests(n: int, seed: int, vocab: int) -> list[tuple[list[int], int]]:
+    """(prompt token ids, output length) of config 5's requests, by the reference's
+    lognormal rule (nanoserve/workload.py:57-75) with random token ids."""
+    rng = np.random.default_rng(seed)
+    p_lens = np.clip(rng.lognormal(np.log(256), 0.7, n).astype(int), 16, 2048)
+    o_lens = np.clip(rng.lognormal(np.log(128), 0.7, n).astype(int), 8, 1024)
+    tok = np.random.default_rng(seed + 1)
+    return [(tok.integers(0, vocab, int(p)).tolist(), int(o)) for p, o in zip(p_lens, o_lens)]
