@@ -116,6 +116,10 @@ class Sequence:
                 f"out={len(self.output_token_ids)}, computed={self.num_computed_tokens})")
 
     @property
+    def prompt_len(self) -> int:
+        return len(self.prompt_token_ids)
+
+    @property
     def num_tokens(self) -> int:
         return len(self.prompt_token_ids) + len(self.output_token_ids)
 
