@@ -333,6 +333,36 @@ int ns_paged_attention(void* out, const void* query,
                        void* workspace, size_t workspace_bytes, void* stream,
                        void* aux_stream, void* fork_event, void* join_event);
 
+/*
+ * ns_paged_attention_noalloc -- ns_paged_attention without a workspace
+ * argument and without any allocation.  No counterpart in the reference: it
+ * is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
+ * and errors as ns_paged_attention, whose kernels it runs, but the split-K
+ * workspace is a 64 MiB array inside the library, one per device, held from
+ * module load until the process ends.  A call whose
+ * ns_paged_attention_workspace_size exceeds 64 MiB returns NS_ERR_WORKSPACE.
+ * The first call on a device looks the array up (and, outside graph
+ * capture, clears it with one fill launch on `stream`); every call leaves it
+ * ready for the next.  All calls on one device share the array, so calls
+ * that overlap in time on one device (different streams) race and must not
+ * be issued.
+ */
+int ns_paged_attention_noalloc(void* out, const void* query,
+                               const void* k_cache, const void* v_cache,
+                               const void* block_tables, int64_t block_table_stride,
+                               int64_t block_table_width, int block_tables_is_int64,
+                               const void* seq_lens, int seq_lens_is_int64,
+                               const void* query_start_loc, int query_start_loc_is_int64,
+                               const void* seq_lens_host, int seq_lens_host_is_int64,
+                               const void* query_start_loc_host, int query_start_loc_host_is_int64,
+                               int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                               int is_decode_only,
+                               int num_heads, int num_kv_heads, int head_dim,
+                               int block_size, int64_t num_blocks,
+                               float scale, int dtype, void* stream,
+                               void* aux_stream, void* fork_event, void* join_event);
+
 #ifdef __cplusplus
 }
 #endif

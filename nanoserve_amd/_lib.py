@@ -122,6 +122,19 @@ SIGNATURES = {
         c_void_p, c_size_t, c_void_p,            # workspace, bytes, stream
         c_void_p, c_void_p, c_void_p,            # aux stream, fork event, join event (all or none)
     ]),
+    "ns_paged_attention_noalloc": (c_int, [
+        c_void_p, c_void_p,                      # out, query
+        c_void_p, c_void_p,                      # k_cache, v_cache
+        c_void_p, c_int64, c_int64, c_int,       # block_tables, row stride, width, is_int64
+        c_void_p, c_int,                         # seq_lens, is_int64
+        c_void_p, c_int,                         # query_start_loc, is_int64
+        c_void_p, c_int,                         # seq_lens_host (host memory, optional), is_int64
+        c_void_p, c_int,                         # query_start_loc_host (host memory, optional), is_int64
+        c_int, c_int64, c_int, c_int, c_int,     # S, T, max_query_len, max_seq_len, decode_only
+        c_int, c_int, c_int, c_int, c_int64,     # Hq, Hkv, D, block_size, num_blocks
+        c_float, c_int, c_void_p,                # scale, dtype, stream
+        c_void_p, c_void_p, c_void_p,            # aux stream, fork event, join event (all or none)
+    ]),
 }
 
 _lock = threading.Lock()

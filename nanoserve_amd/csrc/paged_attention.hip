@@ -19,6 +19,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <utility>
 #include <vector>
 
@@ -1459,22 +1460,64 @@ extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads,
       .total;
 }
 
-extern "C" int ns_paged_attention(void* out, const void* query,
-                                  const void* k_cache, const void* v_cache,
-                                  const void* block_tables, int64_t block_table_stride,
-                                  int64_t block_table_width, int block_tables_is_int64,
-                                  const void* seq_lens, int seq_lens_is_int64,
-                                  const void* query_start_loc, int query_start_loc_is_int64,
-                                  const void* seq_lens_host, int seq_lens_host_is_int64,
-                                  const void* query_start_loc_host, int query_start_loc_host_is_int64,
-                                  int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
-                                  int is_decode_only,
-                                  int num_heads, int num_kv_heads, int head_dim,
-                                  int block_size, int64_t num_blocks,
-                                  float scale, int dtype,
-                                  void* workspace, size_t workspace_bytes, void* stream,
-                                  void* aux_stream, void* fork_event, void* join_event) {
-  using namespace ns;
+namespace ns {
+namespace {
+
+// Scratch of ns_paged_attention_noalloc: the workspace of calls whose caller
+// cannot allocate one.  A file-scope device array, so each device the library
+// runs on holds its own copy from module load (zero-filled by the loader)
+// until the process ends.  In host code `g_noalloc_scratch` names a host-side
+// stand-in, never the device memory: kernels and fills get the address that
+// hipGetSymbolAddress returns for the current device, kept per device.
+constexpr size_t kNoallocScratchBytes = size_t{64} << 20;
+__device__ __align__(256) unsigned char g_noalloc_scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_noalloc_mu;
+void* g_noalloc_ptr[kMaxDevices];
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(u32x4* dst, size_t n16) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += static_cast<size_t>(gridDim.x) * 256)
+    dst[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// The scratch address on the current device, looked up (and, outside graph
+// capture, cleared with a fill kernel on `stream`) on the device's first call.
+// Returns nullptr if the lookup fails.
+void* noalloc_scratch(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_noalloc_mu);
+  if (g_noalloc_ptr[dev]) return g_noalloc_ptr[dev];
+  void* ptr = nullptr;
+  if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(g_noalloc_scratch)) != hipSuccess || !ptr) return nullptr;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cs) == hipSuccess && cs == hipStreamCaptureStatusNone) {
+    // The loader already zero-fills the array; clearing it once more in
+    // stream order costs one launch and makes no assumption about that.
+    u32x4* dst = static_cast<u32x4*>(ptr);
+    size_t n16 = kNoallocScratchBytes / 16;
+    void* args[] = {&dst, &n16};
+    if (hipLaunchKernel(reinterpret_cast<const void*>(&zero_fill_kernel), dim3(1024), dim3(256), args, 0,
+                        stream) != hipSuccess)
+      return nullptr;
+  }
+  g_noalloc_ptr[dev] = ptr;
+  return ptr;
+}
+
+int paged_attention_entry(void* out, const void* query, const void* k_cache, const void* v_cache,
+                          const void* block_tables, int64_t block_table_stride, int64_t block_table_width,
+                          int block_tables_is_int64, const void* seq_lens, int seq_lens_is_int64,
+                          const void* query_start_loc, int query_start_loc_is_int64,
+                          const void* seq_lens_host, int seq_lens_host_is_int64,
+                          const void* query_start_loc_host, int query_start_loc_host_is_int64,
+                          int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                          int is_decode_only, int num_heads, int num_kv_heads, int head_dim,
+                          int block_size, int64_t num_blocks, float scale, int dtype,
+                          void* workspace, size_t workspace_bytes, bool noalloc, void* stream,
+                          void* aux_stream, void* fork_event, void* join_event) {
   if (num_seqs < 0 || num_tokens < 0) return NS_ERR_INVALID_ARG;
   if (num_seqs == 0 || num_tokens == 0) return NS_OK;
   if (!out || !query || !k_cache || !v_cache || !block_tables || !seq_lens) return NS_ERR_INVALID_ARG;
@@ -1507,6 +1550,13 @@ extern "C" int ns_paged_attention(void* out, const void* query,
   const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
   const DecodePlan plan = plan_decode(head_dim, ctx_plan);
   const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan, !is_decode_only);
+  if (noalloc) {
+    // Shapes whose workspace exceeds the scratch are refused before any HIP call.
+    if (wl.total > kNoallocScratchBytes) return NS_ERR_WORKSPACE;
+    workspace = noalloc_scratch(static_cast<hipStream_t>(stream));
+    if (!workspace) return NS_ERR_HIP;
+    workspace_bytes = kNoallocScratchBytes;
+  }
   if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
   // Partials are addressed through buffer descriptors with 32-bit offsets.
   if (wl.pf_part_off - wl.o_off > 0x7FFFFFFFu || wl.pf_part_bytes > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
@@ -1585,4 +1635,54 @@ extern "C" int ns_paged_attention(void* out, const void* query,
     e = head_dim == 64 ? launch_attention<BF16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
                        : launch_attention<BF16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
+}
+
+}  // namespace
+}  // namespace ns
+
+extern "C" int ns_paged_attention(void* out, const void* query,
+                                  const void* k_cache, const void* v_cache,
+                                  const void* block_tables, int64_t block_table_stride,
+                                  int64_t block_table_width, int block_tables_is_int64,
+                                  const void* seq_lens, int seq_lens_is_int64,
+                                  const void* query_start_loc, int query_start_loc_is_int64,
+                                  const void* seq_lens_host, int seq_lens_host_is_int64,
+                                  const void* query_start_loc_host, int query_start_loc_host_is_int64,
+                                  int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                                  int is_decode_only,
+                                  int num_heads, int num_kv_heads, int head_dim,
+                                  int block_size, int64_t num_blocks,
+                                  float scale, int dtype,
+                                  void* workspace, size_t workspace_bytes, void* stream,
+                                  void* aux_stream, void* fork_event, void* join_event) {
+  return ns::paged_attention_entry(out, query, k_cache, v_cache, block_tables, block_table_stride,
+                                   block_table_width, block_tables_is_int64, seq_lens, seq_lens_is_int64,
+                                   query_start_loc, query_start_loc_is_int64, seq_lens_host,
+                                   seq_lens_host_is_int64, query_start_loc_host, query_start_loc_host_is_int64,
+                                   num_seqs, num_tokens, max_query_len, max_seq_len, is_decode_only, num_heads,
+                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, workspace,
+                                   workspace_bytes, false, stream, aux_stream, fork_event, join_event);
+}
+
+extern "C" int ns_paged_attention_noalloc(void* out, const void* query,
+                                          const void* k_cache, const void* v_cache,
+                                          const void* block_tables, int64_t block_table_stride,
+                                          int64_t block_table_width, int block_tables_is_int64,
+                                          const void* seq_lens, int seq_lens_is_int64,
+                                          const void* query_start_loc, int query_start_loc_is_int64,
+                                          const void* seq_lens_host, int seq_lens_host_is_int64,
+                                          const void* query_start_loc_host, int query_start_loc_host_is_int64,
+                                          int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
+                                          int is_decode_only,
+                                          int num_heads, int num_kv_heads, int head_dim,
+                                          int block_size, int64_t num_blocks,
+                                          float scale, int dtype, void* stream,
+                                          void* aux_stream, void* fork_event, void* join_event) {
+  return ns::paged_attention_entry(out, query, k_cache, v_cache, block_tables, block_table_stride,
+                                   block_table_width, block_tables_is_int64, seq_lens, seq_lens_is_int64,
+                                   query_start_loc, query_start_loc_is_int64, seq_lens_host,
+                                   seq_lens_host_is_int64, query_start_loc_host, query_start_loc_host_is_int64,
+                                   num_seqs, num_tokens, max_query_len, max_seq_len, is_decode_only, num_heads,
+                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, nullptr, 0,
+                                   true, stream, aux_stream, fork_event, join_event);
 }
