@@ -452,12 +452,17 @@ def _time_steps(torch, steps, news, K, warmup, stream):
     steps once, so the timed calls are exactly K * calls-per-step calls and
     their bytes are summed exactly."""
     from nanoserve_amd import paged_attention_hip, reshape_and_cache, rope_reshape_and_cache
+    from nanoserve_amd.attention import prepare_decode_plan
 
     calls = [c for st in steps for c in st]
     R, L = len(steps), len(steps[0])
 
     def attn(i):
         c = calls[i]
+        # A step's metadata gets its device-side decode plan once, before its
+        # first layer's call, as the model's forward does (Qwen2Model.forward).
+        if i == 0 or c.md is not calls[i - 1].md:
+            prepare_decode_plan(c.md, c.k_cache)
         return paged_attention_hip(c.query, c.k_cache, c.v_cache, c.md, c.scale)
 
     def write(i):
@@ -646,7 +651,8 @@ def main(argv=None):
             "seeds_timed": res["seeds_timed"],
             "kv_bytes_per_call_mean": res["kv_mean_timed"],
             "timing": "HIP-graph replay of exactly K serving steps cycling the distinct steps, "
-                      "hipEvents on the launch stream",
+                      "hipEvents on the launch stream; each step = one device-side decode-plan launch "
+                      "(ns_paged_decode_plan) + the attention calls, all inside the timed region",
         },
         "us_per_call": round(s_per_call * 1e6, 3),
         "timed_runs_us_per_call": [round(x, 3) for x in res["runs_us_per_call"]],

@@ -250,21 +250,64 @@ int ns_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void
 
 /*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
- * ns_paged_attention needs for these sizes (split-K partials and counters).
- * Without is_decode_only it includes the prefill split state: a fixed 512
- * slots of 40 KiB (head_dim 64) or 72 KiB (head_dim 128).
+ * ns_paged_attention needs for these sizes: arrival counters, a region for
+ * the call's own decode plan, the decode split-K slots and, without
+ * is_decode_only, the prefill split state (512 slots of 40 KiB at head_dim
+ * 64, 72 KiB at 128).  No counterpart in the reference, which allocates per
+ * call.
  *
- * The workspace must be zero-filled once when it is first allocated; every
- * call leaves its counters at zero again, and the counters sit at the same
- * offsets for every call (a fixed 4 MiB head of the workspace), so the same
- * buffer can be reused by later calls of any shape on the same stream
- * without clearing.  Calls that overlap in time (different streams) must use
- * different workspaces.
+ * Layout: an 8 MiB head (arrival counters, a zero page, the plan region),
+ * then the prefill split state (36 MiB, present in every workspace so the
+ * offsets after it never move), then the decode split-K slots.
+ *
+ * The workspace must be zero-filled once when it is first allocated.  Every
+ * call leaves the counters and the prefill split state as it found them
+ * (back at zero: the workgroup that consumes a prefill slot clears it), so
+ * the same buffer serves later calls of any shape on the same stream
+ * without clearing; the decode slots keep the last call's partials, which no
+ * later call reads before writing.  Calls that overlap in time (different
+ * streams) must use different workspaces.
  */
 size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv_heads,
                                          int head_dim, int block_size,
                                          int max_seq_len, int max_query_len,
                                          int64_t num_tokens, int is_decode_only);
+
+/*
+ * ns_paged_decode_plan_size, ns_paged_decode_plan -- the decode work plan of
+ * one step's metadata, built on the device.  No counterpart in the
+ * reference; it is the device-side form of the launch schedule that the
+ * reference's Triton wrapper derives from the device seq_lens on every call
+ * (nanoserve/triton_attention.py:144-160).
+ *
+ * The plan cuts the decode rows (every sequence of a decode-only batch; the
+ * one-query-row sequences of a mixed batch, found from query_start_loc)
+ * into items of context tokens of one (sequence, kv head) pair, sized so
+ * the items about fill the device once for light batches and in several
+ * rounds, longest sequences first, for heavy ones.  Each item also carries
+ * the block ids of its waves' first K/V loads (block size >= 16), so those
+ * loads need no table round trip.  It reads only device memory (seq_lens,
+ * query_start_loc, block_tables), so a captured HIP graph rebuilds it from
+ * the step's lengths and tables on every replay.
+ *
+ * ns_paged_attention builds the plan itself (one extra launch into its
+ * workspace) when it is given none.  The engine's metadata is shared by all
+ * layers of a step, so the shim builds it once per step with
+ * ns_paged_decode_plan and passes it to every layer's call.  A plan is valid
+ * for calls with the same metadata and sizes (num_seqs, num_kv_heads,
+ * head_dim, block_size, max_seq_len, block_table_width, decode-only or not,
+ * and the same device lengths, query offsets and block tables); plan must be
+ * 16-byte aligned with at least ns_paged_decode_plan_size bytes.
+ */
+size_t ns_paged_decode_plan_size(int num_seqs, int num_kv_heads, int head_dim, int block_size,
+                                 int max_seq_len);
+int ns_paged_decode_plan(void* plan, size_t plan_bytes,
+                         const void* block_tables, int64_t block_table_stride,
+                         int64_t block_table_width, int block_tables_is_int64,
+                         const void* seq_lens, int seq_lens_is_int64,
+                         const void* query_start_loc, int query_start_loc_is_int64,
+                         int num_seqs, int is_decode_only, int num_kv_heads, int head_dim,
+                         int block_size, int max_seq_len, void* stream);
 
 /*
  * ns_paged_attention -- unified paged attention (prefill, decode, chunked
@@ -283,23 +326,24 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  * reference decode fast path.  Otherwise query_start_loc delimits each
  * sequence's query rows; sequences with an empty query range are skipped.
  *
- * seq_lens_host (optional, may be NULL) is a HOST copy of seq_lens -- the
- * reference's AttentionMetadata.seq_lens_cpu (attention.py:52-54), which its
- * non-decode path already treats as authoritative (attention.py:124).  It
- * lets the library launch the decode rows as exactly one workgroup per
- * (sequence, kv head, context split), longest sequences first, instead of a
- * grid sized by max_seq_len.  It must equal seq_lens; a device length longer
- * than the host copy makes that decode row's outputs NaN.
+ * Decode rows run as one workgroup per plan item (see
+ * ns_paged_decode_plan): decode_plan, when not NULL, is a plan built for
+ * this call's metadata (decode_plan_bytes its size); NULL makes the call
+ * build one in its workspace first.  A pair cut into several items is merged
+ * inside the launch by the pair's last workgroup to start, in item order,
+ * so results do not depend on timing.
  *
- * query_start_loc_host (optional, may be NULL; read only with seq_lens_host
- * and without is_decode_only) is a HOST copy of query_start_loc -- the
- * reference's AttentionMetadata.query_start_loc_cpu (attention.py:53-54).
- * With it the prefill rows are scheduled exactly: heaviest column blocks
- * first, long key ranges split across workgroups and merged in-launch (the
- * workspace holds the split state), and the decode launch is skipped when no
- * sequence has a single query row.  It must equal query_start_loc; a
- * sequence whose device query length differs has its reached outputs
- * written as NaN (nothing is read or written out of bounds).
+ * seq_lens_host and query_start_loc_host (optional, may be NULL; read only
+ * together and without is_decode_only) are HOST copies of seq_lens and
+ * query_start_loc -- the reference's AttentionMetadata.seq_lens_cpu and
+ * query_start_loc_cpu (attention.py:52-54), which its non-decode path
+ * already treats as authoritative (attention.py:124).  With them the prefill
+ * rows are scheduled exactly: heaviest column blocks first, long key ranges
+ * split across workgroups and merged in-launch (the workspace holds the split
+ * state), and the decode launch is skipped when no sequence has a single
+ * query row.  They must equal the device copies; a sequence whose device
+ * query length differs has its reached outputs written as NaN (nothing is
+ * read or written out of bounds).
  *
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
  * Supported: head_dim in {64, 128}; block_size a power of two;
@@ -330,6 +374,7 @@ int ns_paged_attention(void* out, const void* query,
                        int num_heads, int num_kv_heads, int head_dim,
                        int block_size, int64_t num_blocks,
                        float scale, int dtype,
+                       const void* decode_plan, size_t decode_plan_bytes,
                        void* workspace, size_t workspace_bytes, void* stream,
                        void* aux_stream, void* fork_event, void* join_event);
 
@@ -339,9 +384,9 @@ int ns_paged_attention(void* out, const void* query,
  * is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  Same arguments, results
  * and errors as ns_paged_attention, whose kernels it runs, but the split-K
- * workspace is a 64 MiB array inside the library, one per device, held from
+ * workspace is a 128 MiB array inside the library, one per device, held from
  * module load until the process ends.  A call whose
- * ns_paged_attention_workspace_size exceeds 64 MiB returns NS_ERR_WORKSPACE.
+ * ns_paged_attention_workspace_size exceeds 128 MiB returns NS_ERR_WORKSPACE.
  * The first call on a device looks the array up (and, outside graph
  * capture, clears it with one fill launch on `stream`); every call leaves it
  * ready for the next.  All calls on one device share the array, so calls
@@ -360,7 +405,8 @@ int ns_paged_attention_noalloc(void* out, const void* query,
                                int is_decode_only,
                                int num_heads, int num_kv_heads, int head_dim,
                                int block_size, int64_t num_blocks,
-                               float scale, int dtype, void* stream,
+                               float scale, int dtype,
+                               const void* decode_plan, size_t decode_plan_bytes, void* stream,
                                void* aux_stream, void* fork_event, void* join_event);
 
 #ifdef __cplusplus

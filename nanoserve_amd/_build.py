@@ -22,8 +22,8 @@ CSRC = PKG_DIR / "csrc"
 INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libnanoserve_paged.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["paged_attention.hip", "reshape_and_cache.hip", "rope_cache.hip", "int4_linear.hip",
-           "argmax.hip", "floors.hip"]
+SOURCES = ["paged_attention.hip", "decode_plan.hip", "reshape_and_cache.hip", "rope_cache.hip",
+           "int4_linear.hip", "argmax.hip", "floors.hip"]
 ARCH = "gfx950"
 
 HIPCC_FLAGS = [
@@ -37,6 +37,10 @@ HIPCC_FLAGS = [
     # MFMA accumulators in VGPRs: the softmax rescales them every step, and
     # AGPR accumulators would cost a read and a write per element each time.
     "-mllvm", "-amdgpu-mfma-vgpr-form",
+    # Single-lane atomics stay single-lane: the atomic optimizer turns them
+    # into a wave-wide pattern that reads the result back at once, which
+    # makes the issuing wave wait for every load it has in flight.
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall",
 ]
 

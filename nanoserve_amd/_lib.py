@@ -108,6 +108,14 @@ SIGNATURES = {
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,
     ]),
+    "ns_paged_decode_plan_size": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),  # S, Hkv, D, bs, max_seq_len
+    "ns_paged_decode_plan": (c_int, [
+        c_void_p, c_size_t,                      # plan, bytes
+        c_void_p, c_int64, c_int64, c_int,       # block_tables, row stride, width, is_int64
+        c_void_p, c_int, c_void_p, c_int,        # seq_lens, is_int64, query_start_loc (or None), is_int64
+        c_int, c_int, c_int, c_int, c_int,       # S, decode_only, Hkv, D, block_size
+        c_int, c_void_p,                         # max_seq_len, stream
+    ]),
     "ns_paged_attention": (c_int, [
         c_void_p, c_void_p,                      # out, query
         c_void_p, c_void_p,                      # k_cache, v_cache
@@ -119,6 +127,7 @@ SIGNATURES = {
         c_int, c_int64, c_int, c_int, c_int,     # S, T, max_query_len, max_seq_len, decode_only
         c_int, c_int, c_int, c_int, c_int64,     # Hq, Hkv, D, block_size, num_blocks
         c_float, c_int,                          # scale, dtype
+        c_void_p, c_size_t,                      # decode plan (or None), bytes
         c_void_p, c_size_t, c_void_p,            # workspace, bytes, stream
         c_void_p, c_void_p, c_void_p,            # aux stream, fork event, join event (all or none)
     ]),
@@ -132,7 +141,8 @@ SIGNATURES = {
         c_void_p, c_int,                         # query_start_loc_host (host memory, optional), is_int64
         c_int, c_int64, c_int, c_int, c_int,     # S, T, max_query_len, max_seq_len, decode_only
         c_int, c_int, c_int, c_int, c_int64,     # Hq, Hkv, D, block_size, num_blocks
-        c_float, c_int, c_void_p,                # scale, dtype, stream
+        c_float, c_int,                          # scale, dtype
+        c_void_p, c_size_t, c_void_p,            # decode plan (or None), bytes, stream
         c_void_p, c_void_p, c_void_p,            # aux stream, fork event, join event (all or none)
     ]),
 }

@@ -7,10 +7,12 @@ decode, chunked prefill and mixed batches are one call; query row j of a
 sequence with context length L and query length ql attends to keys
 [0, L - ql + j]; the kv head of query head h is h // (Hq // Hkv).
 
-Everything runs on the GPU through libnanoserve_paged.so: a decode-only batch
-is one kernel launch (split-K partials are merged inside the launch), any
-other batch adds one launch of the variable-length MFMA kernel.  There is no
-torch or Triton fallback; a missing library or an unsupported shape raises.
+Everything runs on the GPU through libnanoserve_paged.so: the decode rows of a
+batch are one kernel launch over a work plan built on the device (once per
+step with `prepare_decode_plan`, else by the call itself), with split-K
+partials merged inside the launch; any other batch adds one launch of the
+variable-length MFMA kernel.  There is no torch or Triton fallback; a missing
+library or an unsupported shape raises.
 """
 
 from __future__ import annotations
@@ -45,6 +47,17 @@ class AttentionMetadata:
     query_lens_cpu: list[int] = None          # type: ignore[assignment]
     seq_lens_cpu: list[int] = None            # type: ignore[assignment]
     query_start_loc_cpu: list[int] = None     # type: ignore[assignment]
+    # The step's device-side decode plan (prepare_decode_plan), built once and
+    # read by every layer's call; None makes each call build its own.
+    decode_plan: "DecodePlan | None" = None
+
+
+@dataclass(frozen=True)
+class DecodePlan:
+    """A device buffer holding ns_paged_decode_plan's output, and the call sizes it is valid for."""
+
+    buffer: torch.Tensor
+    key: tuple
 
 
 _INDEX_DTYPES = (torch.int32, torch.int64)
@@ -107,6 +120,52 @@ def _index(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
     if t.dtype not in _INDEX_DTYPES:
         t = t.to(torch.int64)
     return t
+
+
+def _plan_key(md: AttentionMetadata, num_kv_heads: int, head_dim: int, block_size: int,
+              device: torch.device) -> tuple:
+    """What a plan depends on besides the device lengths it reads: the call sizes
+    and the metadata tensors it was built from."""
+    return (md.num_seqs, num_kv_heads, head_dim, block_size, md.max_seq_len, int(md.block_tables.shape[1]),
+            bool(md.is_decode_only), md.seq_lens.data_ptr(),
+            None if md.query_start_loc is None else md.query_start_loc.data_ptr(), _device_index(device))
+
+
+@torch.inference_mode()
+def prepare_decode_plan(md: AttentionMetadata, cache: torch.Tensor) -> None:
+    """Build md's decode plan on the device (one launch on the current stream)
+    for attention calls over caches shaped like `cache` ([NB, BS, Hkv, D]).
+
+    The reference builds a step's metadata once and hands it to every layer
+    (model_runner.py:85-147, qwen2.py:105-113); the plan belongs to that step
+    in the same way: it is read from the device lengths, so a captured graph
+    that calls this rebuilds it from the replayed step's lengths.  Calls whose
+    sizes differ from the plan's build their own instead.
+    """
+    if md.num_seqs == 0 or md.num_tokens == 0:
+        return
+    lib = _lib.load()
+    _, block_size, num_kv_heads, head_dim = cache.shape
+    device = cache.device
+    bt = _index(md.block_tables, "block_tables", device)
+    sl = _index(md.seq_lens, "seq_lens", device).contiguous()
+    decode_only = bool(md.is_decode_only)
+    qsl_ptr, qsl64 = None, 0
+    if not decode_only:
+        qsl = _index(md.query_start_loc, "query_start_loc", device).contiguous()
+        qsl_ptr, qsl64 = qsl.data_ptr(), int(qsl.dtype == torch.int64)
+    nbytes = int(lib.ns_paged_decode_plan_size(md.num_seqs, num_kv_heads, head_dim, block_size, md.max_seq_len))
+    if nbytes == 0:
+        raise RuntimeError(f"unsupported decode plan shape: Hkv={num_kv_heads} D={head_dim} block_size={block_size}")
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if bt.stride(1) != 1:
+        raise ValueError("block_tables rows must be contiguous")
+    rc = lib.ns_paged_decode_plan(buf.data_ptr(), nbytes, bt.data_ptr(), bt.stride(0), bt.shape[1],
+                                  int(bt.dtype == torch.int64), sl.data_ptr(), int(sl.dtype == torch.int64),
+                                  qsl_ptr, qsl64, md.num_seqs, int(decode_only), num_kv_heads, head_dim,
+                                  block_size, md.max_seq_len, torch.cuda.current_stream(device).cuda_stream)
+    _lib.check(rc, "ns_paged_decode_plan")
+    md.decode_plan = DecodePlan(buf, _plan_key(md, num_kv_heads, head_dim, block_size, device))
 
 
 def workspace_bytes(md: AttentionMetadata, num_heads: int, num_kv_heads: int,
@@ -197,6 +256,9 @@ def paged_attention_hip(
             f"block_size={block_size}")
     ws = _workspace(device, stream, nbytes)
     aux = (None, None, None) if decode_only else _aux_stream(device, stream)
+    plan = md.decode_plan
+    if plan is not None and plan.key != _plan_key(md, num_kv_heads, head_dim, block_size, device):
+        plan = None  # built for other sizes: the call plans for itself
 
     rc = lib.ns_paged_attention(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
@@ -208,9 +270,14 @@ def paged_attention_hip(
         md.num_seqs, num_tokens, md.max_query_len, md.max_seq_len, int(decode_only),
         num_heads, num_kv_heads, head_dim, block_size, num_blocks,
         float(scale), _lib.DTYPE_CODES[q.dtype],
+        None if plan is None else plan.buffer.data_ptr(), 0 if plan is None else plan.buffer.numel(),
         ws.data_ptr(), ws.numel(), stream, *aux)
     _lib.check(rc, "ns_paged_attention")
     return out.view(query.shape)
+
+
+# The per-step hook a forward calls once before its layers (Qwen2Model.forward).
+paged_attention_hip.prepare = prepare_decode_plan
 
 
 def get_attention_backend(name: str = "auto"):

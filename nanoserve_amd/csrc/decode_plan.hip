@@ -1,0 +1,325 @@
+// Device-side decode plan: turns the batch's device lengths into the decode
+// kernel's work items (decode_plan.h).
+//
+// 1. Each sequence's context length, clamped to the table, and whether it is
+//    a decode row (one query row; every row of a decode-only batch).
+// 2. Tokens per item, T: the smallest multiple of 16, at least min_tokens,
+//    for which Hkv * sum_s max(1, ceil(L_s / T)) items fit the target of
+//    `cus` x rounds items (rounds = work / (cus x round_tokens), at most the
+//    host's bound); when even the largest T (the longest context, at most
+//    kMaxItemTokens) does not fit, T is that largest value.  Sequence s is
+//    cut into n_s = max(1, ceil(L_s / T)) ranges of equal 16-aligned size.
+// 3. Pairs are listed longest sequence first (so the dispatcher starts the
+//    long pairs, whose merges finish last, first), the n_s items of each
+//    (sequence, kv head) pair next to each other.
+// 4. Every item carries the block ids of its waves' first steps.
+//
+// Batches of up to kLdsSeqs sequences: every workgroup of the grid computes
+// steps 1-3 in its own LDS (the same result everywhere: they read the same
+// lengths) and writes its own slice of the items, so the block-id reads of
+// step 4 are spread over the device.  Larger batches run one workgroup that
+// keeps its per-sequence arrays in scratch after the items and lists them in
+// batch order.
+#include "decode_plan.h"
+#include "ns_common.h"
+
+namespace ns {
+namespace {
+
+constexpr int kThreads = 256;           // threads of a plan workgroup
+constexpr int kWaves = kThreads / 64;
+constexpr int kLdsSeqs = 2048;          // batches held in LDS
+constexpr int kEntryPasses = 4;         // items of 32 entries per thread pass: kThreads / 32 per pass
+constexpr int kItemsPerGroup = kThreads / 32 * kEntryPasses;
+
+__device__ __forceinline__ uint32_t wave_sum32(uint32_t v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum64(uint64_t v) {
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+__device__ __forceinline__ uint32_t wave_max32(uint32_t v) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const uint32_t o = __shfl_xor(v, off);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Exclusive prefix sum of v over the workgroup in thread order; `total` gets
+// the workgroup's sum.  `red` holds one word per wave.
+__device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& total, uint32_t* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint32_t x = v;
+  for (int off = 1; off < 64; off <<= 1) {
+    const uint32_t y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) red[w] = x;
+  __syncthreads();
+  uint32_t before = 0, all = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    const uint32_t t = red[k];
+    before += k < w ? t : 0u;
+    all += t;
+  }
+  __syncthreads();
+  total = all;
+  return before + x - v;
+}
+
+// Ranges of a context of L tokens at T tokens per item (an empty context is
+// one empty item).
+__device__ __forceinline__ uint32_t items_of(uint32_t L, uint32_t T) { return L <= T ? 1u : (L + T - 1) / T; }
+
+struct alignas(16) PlanShared {
+  uint64_t red64[kWaves];
+  uint32_t red[kWaves], red2[kWaves];
+  uint32_t fits[kWaves];
+  int32_t len[kLdsSeqs], order[kLdsSeqs], qtok[kLdsSeqs];
+  int32_t first[kLdsSeqs + 1];
+};
+
+__global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a, int items_per_group) {
+  __shared__ PlanShared sh;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int S = a.num_seqs, Hkv = a.num_kv_heads;
+  auto* hdr = static_cast<DecodePlanHeader*>(a.plan);
+  auto* items = reinterpret_cast<DecodeItem*>(hdr + 1);
+  // Per-sequence arrays: length (-1: not a decode row), query row, sequences
+  // in list order, and the first item of the r-th listed sequence.
+  const bool in_lds = S <= kLdsSeqs;
+  int32_t* g_scratch = reinterpret_cast<int32_t*>(items + a.item_cap);
+  int32_t* lens = in_lds ? sh.len : g_scratch;
+  int32_t* qtok = in_lds ? sh.qtok : g_scratch + S;
+  int32_t* order = in_lds ? sh.order : g_scratch + 2 * S;
+  int32_t* firstr = in_lds ? sh.first : g_scratch + 3 * S;  // S + 1 entries: the last is the item count
+
+  // 1. Lengths and query rows.
+  uint64_t work = 0;
+  uint32_t active = 0, max_len = 0;
+  for (int s = tid; s < S; s += kThreads) {
+    int64_t L = load_index(a.seq_lens, s, a.sl64);
+    L = L < 0 ? 0 : (L < a.max_ctx ? L : a.max_ctx);
+    int64_t q = s;
+    bool on = true;
+    if (!a.decode_only) {
+      q = load_index(a.qsl, s, a.qsl64);
+      on = load_index(a.qsl, s + 1, a.qsl64) - q == 1;
+    }
+    lens[s] = on ? static_cast<int32_t>(L) : -1;
+    qtok[s] = static_cast<int32_t>(q);
+    if (on) {
+      work += static_cast<uint64_t>(L);
+      active += 1;
+      max_len = static_cast<uint32_t>(L) > max_len ? static_cast<uint32_t>(L) : max_len;
+    }
+  }
+  work = wave_sum64(work);
+  active = wave_sum32(active);
+  max_len = wave_max32(max_len);
+  if (lane == 0) {
+    sh.red64[w] = work;
+    sh.red[w] = active;
+    sh.red2[w] = max_len;
+  }
+  __syncthreads();  // also publishes lens / qtok
+  work = 0;
+  active = 0;
+  max_len = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    work += sh.red64[k];
+    active += sh.red[k];
+    max_len = sh.red2[k] > max_len ? sh.red2[k] : max_len;
+  }
+  const int64_t pair_work = static_cast<int64_t>(work) * Hkv;
+  const int64_t pairs = static_cast<int64_t>(active) * Hkv;
+
+  // 2. Tokens per item, in units of 16 tokens.  The item count at T is at
+  // least Hkv * work / T and at most Hkv * (work / T + active), so the
+  // smallest fitting T lies in [ca, cb]; the waves search it nw points at a
+  // time.
+  const int64_t per_round = static_cast<int64_t>(a.cus) * a.round_tokens;
+  int64_t rounds = (pair_work + per_round - 1) / per_round;
+  rounds = rounds < 1 ? 1 : (rounds > a.rounds ? a.rounds : rounds);
+  const int64_t target = static_cast<int64_t>(a.cus) * rounds;
+  const int64_t lo = (a.min_tokens + 15) / 16;
+  int64_t hi = (static_cast<int64_t>(max_len) + 15) / 16;
+  hi = hi < lo ? lo : (hi > kMaxItemTokens / 16 ? kMaxItemTokens / 16 : hi);
+  auto clamp = [&](int64_t x) { return x < lo ? lo : (x > hi ? hi : x); };
+  int64_t ca = clamp((pair_work + 16 * target - 1) / (16 * target));  // 16 * ca >= Hkv * work / target
+  int64_t cb = hi;
+  if (pairs < target) {
+    const int64_t room = target - pairs;
+    cb = clamp((pair_work + 16 * room - 1) / (16 * room));  // Hkv * (work / T + active) <= target
+  }
+  // Smallest fitting point of [ca, cb], or cb when none fits (cb is hi then).
+  while (ca < cb) {
+    const int64_t step = (cb - ca + kWaves - 1) / kWaves;
+    const int64_t pt = ca + static_cast<int64_t>(w) * step;
+    uint32_t n = 0;
+    if (pt < cb) {
+      const uint32_t T = static_cast<uint32_t>(pt * 16);
+      for (int s = lane; s < S; s += 64) {
+        const int32_t L = lens[s];
+        if (L >= 0) n += items_of(static_cast<uint32_t>(L), T);
+      }
+      n = wave_sum32(n);
+    }
+    if (lane == 0) sh.fits[w] = pt < cb && static_cast<int64_t>(n) * Hkv <= target;
+    __syncthreads();
+    int k = kWaves;
+#pragma unroll
+    for (int j = kWaves - 1; j >= 0; --j)
+      if (sh.fits[j]) k = j;
+    __syncthreads();  // fits is rewritten by the next pass
+    if (k == 0) {
+      cb = ca;
+    } else if (k < kWaves) {  // in (point k - 1, point k]
+      cb = ca + static_cast<int64_t>(k) * step;
+      ca += static_cast<int64_t>(k - 1) * step + 1;
+    } else {  // past the last point evaluated (the points below cb)
+      int64_t m = (cb - ca - 1) / step;
+      m = m < kWaves - 1 ? m : kWaves - 1;
+      ca += m * step + 1;
+    }
+  }
+  const uint32_t T = static_cast<uint32_t>(ca * 16);
+
+  // 3. List order: by decreasing length (ties by index) for batches held in
+  // LDS, else batch order; sequences that are not decode rows drop out.
+  if (in_lds) {
+    for (int s = tid; s < S; s += kThreads) {
+      const int32_t L = lens[s];
+      if (L < 0) continue;
+      int r = 0;
+      int j = 0;
+      for (; j + 4 <= S; j += 4) {
+        const int4 l4 = *reinterpret_cast<const int4*>(lens + j);
+        r += (l4.x > L || (l4.x == L && j < s)) + (l4.y > L || (l4.y == L && j + 1 < s)) +
+             (l4.z > L || (l4.z == L && j + 2 < s)) + (l4.w > L || (l4.w == L && j + 3 < s));
+      }
+      for (; j < S; ++j) {
+        const int32_t Lj = lens[j];
+        r += Lj > L || (Lj == L && j < s);
+      }
+      order[r] = s;
+    }
+  } else {
+    uint32_t base = 0;
+    for (int s0 = 0; s0 < S; s0 += kThreads) {
+      const int s = s0 + tid;
+      const uint32_t on = s < S && lens[s] >= 0;
+      uint32_t tot;
+      const uint32_t r = base + block_exclusive_scan(on, tot, sh.red);
+      if (on) order[r] = s;
+      base += tot;
+    }
+  }
+  __syncthreads();
+
+  // 4. First item of each listed sequence: prefix sums of Hkv * n_s.
+  uint32_t base = 0;
+  for (int r0 = 0; r0 < static_cast<int>(active); r0 += kThreads) {
+    const int r = r0 + tid;
+    const uint32_t n = r < static_cast<int>(active) ? items_of(lens[order[r]], T) * Hkv : 0u;
+    uint32_t tot;
+    const uint32_t f = base + block_exclusive_scan(n, tot, sh.red);
+    if (r < static_cast<int>(active)) firstr[r] = static_cast<int32_t>(f);
+    base += tot;
+  }
+  const uint32_t n_items = base < a.item_cap ? base : a.item_cap;
+  if (tid == 0) firstr[active] = static_cast<int32_t>(base);
+  __syncthreads();
+
+  // 5. This workgroup's items, 32 threads per item: thread e of an item
+  // writes header word e (e < 8) and block-id entry e.  Every pass covers
+  // kThreads / 32 items; the passes' block-table loads go out together.
+  const int NT = a.tiles_per_step;
+  const int IS = kItemBlocks / (kItemWaves * NT);
+  const bool inline_blocks = a.bs_shift >= 4;
+  const int e = tid & 31;
+  const int ew = e / (IS * NT), est = e / NT % IS, ej = e % NT;  // entry e: tile ej of step est of wave ew
+  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * items_per_group;
+  int64_t g1 = g0 + items_per_group;
+  g1 = g1 < n_items ? g1 : n_items;
+  for (int64_t i0 = g0; i0 < g1; i0 += kThreads / 32 * kEntryPasses) {
+    uint32_t hw[kEntryPasses];
+    int64_t id[kEntryPasses];
+    int64_t at[kEntryPasses];
+#pragma unroll
+    for (int ps = 0; ps < kEntryPasses; ++ps) {
+      const int64_t idx = i0 + ps * (kThreads / 32) + (tid >> 5);
+      at[ps] = idx < g1 ? idx : -1;
+      hw[ps] = 0;
+      id[ps] = 0;
+      if (idx >= g1) continue;
+      int lo_r = 0, hi_r = static_cast<int>(active) - 1;
+      while (lo_r < hi_r) {
+        const int mid = (lo_r + hi_r + 1) >> 1;
+        if (firstr[mid] <= idx) lo_r = mid;
+        else hi_r = mid - 1;
+      }
+      const int s = order[lo_r];
+      const uint32_t L = static_cast<uint32_t>(lens[s]);
+      const uint32_t n = items_of(L, T);
+      const uint32_t rel = static_cast<uint32_t>(idx - firstr[lo_r]);
+      const uint32_t h = rel / n, k = rel % n;
+      const uint32_t size = n == 1 ? L : ((L + n - 1) / n + 15) / 16 * 16;
+      const uint32_t t0 = k * size;
+      const uint32_t t1 = k + 1 == n ? L : (t0 + size < L ? t0 + size : L);
+      // DecodeItem{s, qtok, t0, t1, first, nsplit, kvh, split}.
+      const uint32_t fields[8] = {static_cast<uint32_t>(s), static_cast<uint32_t>(qtok[s]), t0, t1,
+                                  static_cast<uint32_t>(idx) - k, n, h, k};
+#pragma unroll
+      for (int f = 0; f < 8; ++f)
+        if (e == f) hw[ps] = fields[f];
+      // Wave ew's tokens are [t0 + ew * per_wave, ...) in steps of 16 * NT.
+      const uint32_t tiles = (t1 - t0 + 15) >> 4;
+      const uint32_t per_wave = (tiles + kItemWaves - 1) / kItemWaves * 16;
+      const uint32_t t = t0 + ew * per_wave + 16 * (est * NT + ej);
+      if (inline_blocks && t < t1 && t < t0 + (ew + 1) * per_wave) {
+        const int64_t row = static_cast<int64_t>(s) * a.bt_stride;
+        id[ps] = load_index(a.block_tables, row + (t >> a.bs_shift), a.bt64);
+      }
+    }
+#pragma unroll
+    for (int ps = 0; ps < kEntryPasses; ++ps) {
+      if (at[ps] < 0) continue;
+      uint32_t* dst = reinterpret_cast<uint32_t*>(items + at[ps]);
+      const int64_t v = id[ps];
+      const int32_t b = v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : static_cast<int32_t>(v));
+      if (e < 8) dst[e] = hw[ps];
+      dst[8 + e] = static_cast<uint32_t>(b);
+    }
+  }
+  if (blockIdx.x == 0 && tid < 4) {
+    // DecodePlanHeader{n_items, num_seqs, num_kv_heads, item_tokens, item_cap, 0...}.
+    u32x4* dst = reinterpret_cast<u32x4*>(hdr);
+    dst[tid] = tid == 0 ? u32x4{n_items, static_cast<uint32_t>(S), static_cast<uint32_t>(Hkv), T}
+                        : (tid == 1 ? u32x4{a.item_cap, 0u, 0u, 0u} : u32x4{0u, 0u, 0u, 0u});
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode_plan(const DecodePlanArgs& a, hipStream_t stream) {
+  DecodePlanArgs args = a;
+  // Batches held in LDS spread the items over a grid; larger ones use one
+  // workgroup (their per-sequence scratch is shared).
+  int per_group = kItemsPerGroup;
+  int grid = static_cast<int>((static_cast<int64_t>(a.item_cap) + per_group - 1) / per_group);
+  if (a.num_seqs > kLdsSeqs || grid < 1) {
+    grid = 1;
+    per_group = static_cast<int>(a.item_cap);
+  }
+  void* kargs[] = {&args, &per_group};
+  return hipLaunchKernel(reinterpret_cast<const void*>(&decode_plan_kernel), dim3(grid), dim3(kThreads), kargs, 0,
+                         stream);
+}
+
+}  // namespace ns

@@ -23,6 +23,7 @@
 #include <utility>
 #include <vector>
 
+#include "decode_plan.h"
 #include "ns_common.h"
 
 namespace ns {
@@ -30,7 +31,6 @@ namespace {
 
 // Plan entries carried in the kernel arguments (keeps them under 4 KiB).
 constexpr int kPlanMax = 768;
-constexpr uint32_t kPlanEmpty = 0xFFFFFFFFu;  // plan slot with no work (sequence ids stay below 0xFFFF)
 
 struct AttnParams {
   char* out;
@@ -43,40 +43,40 @@ struct AttnParams {
   const void* qsl;
   int bt64, sl64, qsl64;
   int decode_only;
+  int num_seqs;
   int64_t num_tokens;     // rows of query/out; query rows outside are never touched
   int num_heads, num_kv_heads, group;
   int bs_shift;
   int64_t num_blocks;
   int64_t max_ctx;        // tokens addressable through a table row
   float scale_log2;       // scale * log2(e): softmax runs in base 2
-  int split_tokens;       // decode: context tokens per workgroup (pair plans: the base, shifted per pair)
-  int split_tokens_max;   // decode, host side: the longest split any workgroup takes
-  int max_splits;         // decode: workgroups per (sequence, kv head)
   int skip_decode_rows;   // varlen: one-row sequences belong to the decode kernel
-  float* part_o;          // [S, Hkv, max_splits, G, D]  unnormalised partial outputs
-  float* part_ml;         // [S, Hkv, max_splits, G, 2]  (running max, running sum)
-  int part_o_bytes, part_ml_bytes;
+  // Decode: the plan (decode_plan.h) and the split-K state.  Partial slot i
+  // (of plan item i) is slot_words 32-bit words of `part` (part_bytes in all).
+  const DecodePlanHeader* plan_hdr;
+  const DecodeItem* items;
+  int64_t item_cap;
+  int inline_blocks;      // items carry their waves' first-steps block ids (block size >= 16)
+  const void* zeros;      // kZeroPageBytes of the workspace head that are never written
+  uint32_t* part;
+  int part_bytes;
+  int slot_words;
   unsigned* counters;     // [S, Hkv] arrivals per (sequence, kv head); left at zero
   // Prefill split-K: partial slots of one workgroup's columns each, and one
   // arrival counter per split (sequence, kv head, column block); left at zero.
   float* pf_part;
   int pf_part_bytes;
   unsigned* pf_counters;
-  int plan_n;             // decode: workgroups in the planned grid; prefill: sequences listed (0: no plan)
-  int plan_pairs;         // decode: 0 = one plan entry per workgroup, else pairs listed
-  // Decode schedule from host-side lengths, either one entry per workgroup x,
-  // s | kvh << 16 | split << 20 | (nsplit - 1) << 26 or kPlanEmpty, or (long
-  // contexts) one entry pair per (sequence, kv head): plan[0..8] are the
-  // per-XCD offsets into the pair list, pair k is plan[9 + 2k] = s | kvh << 16 |
-  // (nsplit - 1) << 20 and plan[10 + 2k] = its first workgroup index on its XCD.
-  // Prefill schedule (its own copy of the parameters): two entries per listed
-  // sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
-  // slot_base | pair_base << 16.
+  int plan_n;             // prefill: sequences listed (0: no plan)
+  // Prefill schedule from host-side lengths and query offsets: two entries per
+  // listed sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
+  // slot_base | pair_base << 16, then its query length.
   uint32_t plan[kPlanMax];
 };
 
 // --------------------------------------------------------------------------
-// Decode: one workgroup of W waves per (sequence, kv head, context split).
+// Decode: one workgroup of W waves per plan item (a token range of one
+// (sequence, kv head) pair); the grid loops over the plan's items.
 // --------------------------------------------------------------------------
 template <int D, int W, int CH_>
 struct DecodeCfg {
@@ -93,24 +93,12 @@ struct DecodeCfg {
   static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
 };
 
-// Split-K partials.  Split sp of pair (sequence, kv head) stores, for each
-// query head col of the group, its running (max, sum) at
-//   part_ml[2 * ((pair * max_splits + sp) * G + col) + {0, 1}]
-// and its unnormalised output at
-//   part_o[((pair * max_splits + sp) * G + col) * D + d].
-//
-// Partials cross workgroups (and XCDs, whose L2s are not coherent with each
-// other) through device-scope (sc1) buffer accesses: the stores write through
-// to the device coherence point and the loads bypass the non-coherent caches,
-// so the only ordering the merge needs is that a workgroup's stores are
-// acknowledged (s_waitcnt vmcnt(0)) before its arrival is counted.  No L2
-// writeback or invalidate is issued.
+// Split-K state crosses workgroups (and XCDs, whose L2s are not coherent
+// with each other) through device-scope accesses: stores with the SC1 cache
+// policy write through to the device coherence point, and agent-scope atomic
+// loads read from it.  No L2 writeback or invalidate is issued.
 constexpr int kSc1 = 16;                      // cache-policy bit SC1 of gfx94x/gfx950 buffer ops
 constexpr int kBufferWord3 = 0x00020000;      // raw 32-bit buffer descriptor, word 3
-
-struct PartBuffers {
-  __amdgpu_buffer_rsrc_t ml, o;
-};
 
 // 32-bit device-scope buffer load.  Wider partial loads are written as runs
 // of these, which the backend merges into dwordx2/x4: with ROCm 7.2's clang,
@@ -119,13 +107,6 @@ struct PartBuffers {
 // dword), while b32 loads merge and narrow correctly.
 __device__ __forceinline__ float ld_sc1(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kSc1));
-}
-
-__device__ __forceinline__ PartBuffers part_buffers(const AttnParams& p) {
-  PartBuffers b;
-  b.ml = __builtin_amdgcn_make_buffer_rsrc(p.part_ml, static_cast<short>(0), p.part_ml_bytes, kBufferWord3);
-  b.o = __builtin_amdgcn_make_buffer_rsrc(p.part_o, static_cast<short>(0), p.part_o_bytes, kBufferWord3);
-  return b;
 }
 
 __device__ __forceinline__ void merge_into(float& m, float& l, floatx4& o, float m2, float l2, floatx4 o2) {
@@ -137,51 +118,76 @@ __device__ __forceinline__ void merge_into(float& m, float& l, floatx4& o, float
   m = mn;
 }
 
-// Combine the nsplit partials of one pair into out_row ([G, D] of this kv
-// head's query heads).  Each float4 column (head, 4 dims) is owned by tpi
-// consecutive lanes that walk disjoint split subsets with up to 8 loads in
-// flight each, then merge by butterfly; the order of operations is fixed, so
-// the result does not depend on timing.
+template <class IDX>
+__device__ __forceinline__ int64_t ld_idx(const void* p, int64_t i) {
+  return static_cast<int64_t>(reinterpret_cast<const IDX*>(p)[i]);
+}
+
+// Split-K partials.  Plan item i of a pair that has several items owns slot i
+// of `part`: slot_words 32-bit words holding, for each query head col of the
+// group, its unnormalised output at word col * D + d and its running (max in
+// log2 units, sum) at words G * D + 2 * col + {0, 1}.
+//
+// Merge protocol: the pair's last workgroup to FINISH merges.  Every item
+// stores its partial at device scope (sc1), waits until the stores are
+// acknowledged, and only then adds one to the pair's arrival count; the item
+// whose add returns nsplit - 1 has every partial visible, reads them back
+// (sc1) and folds them in split order, so the result does not depend on
+// which workgroup merges, then sets the count back to zero for the next
+// call.  Nobody waits for another workgroup, so the merge never stalls on a
+// straggler: it happens when the last one arrives.
+//
+// The merger's reads: each float4 column (head, 4 dims) of the output is
+// owned by tpi consecutive lanes that walk disjoint split subsets with up to
+// 8 loads in flight each, then combine by butterfly; the order of operations
+// is fixed by tpi and nsplit alone.
 template <class DT, int D, int THREADS>
-__device__ void merge_splits(const AttnParams& p, const PartBuffers& pb, int64_t pair, int nsplit,
-                             typename DT::T* out_row) {
+__device__ void merge_partials(const AttnParams& p, __amdgpu_buffer_rsrc_t pr, uint32_t first, int nsplit,
+                               typename DT::T* out_row) {
   using T = typename DT::T;
   const int G = p.group;
   const int items = G * (D / 4);
+  const int slot_words = p.slot_words;
   int tpi = THREADS / items;
   tpi = tpi >= 8 ? 8 : tpi >= 4 ? 4 : tpi >= 2 ? 2 : 1;
   const int tid = threadIdx.x, sub = tid % tpi;
-  const int64_t base = pair * p.max_splits;
   for (int it = tid / tpi; it < items; it += THREADS / tpi) {
     // The lanes of a tpi group share `it`, so they run the same trip count
     // and are all active at the butterfly below.
     const int col = it / (D / 4), d4 = it % (D / 4);
+    const int o_word = col * D + 4 * d4, ml_word = G * D + 2 * col;
     float m = -INFINITY, l = 0.f;
     floatx4 o = {0.f, 0.f, 0.f, 0.f};
+    int poison = 0;
     for (int sp0 = sub; sp0 < nsplit; sp0 += 8 * tpi) {
       float mb[8], lb[8];
       floatx4 ob[8];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        // Slots past nsplit read split 0 again (in bounds) and are dropped below.
+        // Slots past nsplit read the pair's first slot again (in bounds) and are dropped below.
         const int sp = sp0 + k * tpi < nsplit ? sp0 + k * tpi : 0;
-        const int pi = static_cast<int>((base + sp) * G + col);
-        mb[k] = ld_sc1(pb.ml, pi * 8);
-        lb[k] = ld_sc1(pb.ml, pi * 8 + 4);
-        const int oo = pi * (D * 4) + 16 * d4;
-        ob[k] = floatx4{ld_sc1(pb.o, oo), ld_sc1(pb.o, oo + 4), ld_sc1(pb.o, oo + 8), ld_sc1(pb.o, oo + 12)};
+        const int base = (static_cast<int>(first) + sp) * slot_words;
+        mb[k] = ld_sc1(pr, 4 * (base + ml_word));
+        lb[k] = ld_sc1(pr, 4 * (base + ml_word + 1));
+        const int ob4 = 4 * (base + o_word);
+        ob[k] = floatx4{ld_sc1(pr, ob4), ld_sc1(pr, ob4 + 4), ld_sc1(pr, ob4 + 8), ld_sc1(pr, ob4 + 12)};
       }
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        if (sp0 + k * tpi < nsplit) merge_into(m, l, o, mb[k], lb[k], ob[k]);
+        if (sp0 + k * tpi < nsplit) {
+          poison |= lb[k] != lb[k];
+          merge_into(m, l, o, mb[k], lb[k], ob[k]);
+        }
     }
     for (int off = 1; off < tpi; off <<= 1) {
       const float m2 = __shfl_xor(m, off), l2 = __shfl_xor(l, off);
       const floatx4 o2 = {__shfl_xor(o[0], off), __shfl_xor(o[1], off), __shfl_xor(o[2], off), __shfl_xor(o[3], off)};
+      poison |= __shfl_xor(poison, off);
       merge_into(m, l, o, m2, l2, o2);
     }
     if (sub == 0) {
       // A split that met an invalid block id carries NaN, which propagates.
+      if (poison) l = NAN;
       const float inv = l > 0.f || l != l ? 1.f / l : 0.f;
       typename DT::vec4 v4;
 #pragma unroll
@@ -191,90 +197,72 @@ __device__ void merge_splits(const AttnParams& p, const PartBuffers& pb, int64_t
   }
 }
 
-template <class IDX>
-__device__ __forceinline__ int64_t ld_idx(const void* p, int64_t i) {
-  return static_cast<int64_t>(reinterpret_cast<const IDX*>(p)[i]);
+// One plan item: context tokens [t0, t1) of (sequence s, kv head), read once
+// and used by all G query heads of the group.  The item's 16-token tiles are
+// dealt out evenly, each wave a contiguous run walked CH tokens per step with
+// the next step's K/V loads (and the step after's table entries) in flight.
+// A wave's share of an item's carried block ids: steps IS of NT tiles.
+template <int W, int CH>
+struct WaveBlocks {
+  static constexpr int NT = CH / 16;
+  static constexpr int IS = kItemBlocks / (W * NT);
+  static constexpr int N = IS * NT;
+  static_assert(N == 8, "two 16-byte rows per wave");
+  int32_t id[N];
+};
+
+// The item rows and this wave's carried block ids of plan item idx (uniform
+// per wave, so they come through the scalar cache, outside the vector-memory
+// order the K/V loads keep).
+template <int W, int CH>
+__device__ __forceinline__ void load_item(const AttnParams& p, uint32_t idx, u32x4& r0, u32x4& r1,
+                                          WaveBlocks<W, CH>& wb) {
+  const u32x4* rows = reinterpret_cast<const u32x4*>(p.items + idx);
+  r0 = rows[0];
+  r1 = rows[1];
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const u32x4* ib = rows + 2 + wave * 2;
+  const u32x4 a = ib[0], b = ib[1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    wb.id[e] = static_cast<int32_t>(a[e]);
+    wb.id[4 + e] = static_cast<int32_t>(b[e]);
+  }
 }
 
-// Decode.  Work unit: (sequence s, kv head, split) = split_tokens consecutive
-// context tokens of one kv head, read once and used by all G query heads of
-// the group.  With a host plan the grid is (plan_n) and entry x names
-// (s, kv head, split, nsplit): all splits of a pair sit on workgroup ids with
-// the same x % 8, i.e. on one XCD, so the merging workgroup reads the
-// partials from its own L2 (the protocol does not depend on that placement,
-// only its speed does).  Otherwise the grid is (max_splits, Hkv, S) and splits
-// past a sequence's end exit at once.
-template <class DT, int D, int W, int CH, class BTI, bool PIPE>
-__global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
+template <class DT, int D, int W, int CH, class BTI, bool BIG>
+__device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u32x4 r0, u32x4 r1,
+                                            const WaveBlocks<W, CH>& ib, char* smem, int64_t* later_lds,
+                                            int& s_merger) {
   using Cfg = DecodeCfg<D, W, CH>;
   using T = typename DT::T;
   using V8 = typename DT::vec8;
   constexpr int THREADS = Cfg::kThreads;
   constexpr int NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, VT_LD = Cfg::VT_LD;
-  __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
-  __shared__ int s_last;
+  constexpr int IS = WaveBlocks<W, CH>::IS;
+  static_assert(W == kItemWaves, "items carry the block ids of kItemWaves waves");
 
-  int s, split, kvh, nsplit_plan = 0;
-  int split_tok = p.split_tokens;
-  if (p.plan_n > 0 && p.plan_pairs == 0) {
-    const uint32_t e = p.plan[blockIdx.x];
-    if (e == kPlanEmpty) return;
-    s = static_cast<int>(e & 0xFFFFu);
-    kvh = static_cast<int>((e >> 16) & 0xFu);
-    split = static_cast<int>((e >> 20) & 0x3Fu);
-    nsplit_plan = static_cast<int>(e >> 26) + 1;
-  } else if (p.plan_n > 0) {
-    // Pair list: workgroup x is the (x / 8)-th of XCD x % 8; find the pair
-    // whose splits cover it (binary search over first-workgroup indices).
-    const int x = static_cast<int>(blockIdx.x & 7u), idx = static_cast<int>(blockIdx.x >> 3);
-    int lo = static_cast<int>(p.plan[x]), hi = static_cast<int>(p.plan[x + 1]);
-    if (lo >= hi) return;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (static_cast<int>(p.plan[10 + 2 * mid] & 0x3FFFFFFu) <= idx) lo = mid;
-      else hi = mid;
-    }
-    const uint32_t e = p.plan[9 + 2 * lo], f = p.plan[10 + 2 * lo];
-    nsplit_plan = static_cast<int>(e >> 20) + 1;
-    split = idx - static_cast<int>(f & 0x3FFFFFFu);
-    split_tok = p.split_tokens << (f >> 26);
-    if (split >= nsplit_plan) return;  // past the last pair of this XCD
-    s = static_cast<int>(e & 0xFFFFu);
-    kvh = static_cast<int>((e >> 16) & 0xFu);
-  } else {
-    split = blockIdx.x;
-    kvh = blockIdx.y;
-    s = blockIdx.z;
-  }
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int s = static_cast<int>(r0[0]);
+  const int64_t qtok = r0[1], t0 = r0[2], t1 = r0[3];
+  const uint32_t first = r1[0];
+  const int nsplit = static_cast<int>(r1[1]), kvh = static_cast<int>(r1[2]), split = static_cast<int>(r1[3]);
   const int G = p.group, Hkv = p.num_kv_heads;
+  // A plan that does not belong to this call is skipped, never followed out of bounds.
+  if (static_cast<uint32_t>(s) >= static_cast<uint32_t>(p.num_seqs) || kvh >= Hkv || qtok >= p.num_tokens ||
+      t1 < t0 || t1 > p.max_ctx || nsplit < 1 || split >= nsplit || first + static_cast<uint32_t>(split) != idx ||
+      static_cast<int64_t>(first) + nsplit > p.item_cap)
+    return;
+
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
+
   const int bs_mask = (1 << p.bs_shift) - 1;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
-  const int64_t t_split0 = static_cast<int64_t>(split) * split_tok;
-  const int64_t t_cap = p.max_ctx < t_split0 + split_tok ? p.max_ctx : t_split0 + split_tok;
+  const int64_t tiles = (t1 - t0 + 15) >> 4;
+  const int64_t per_wave = (tiles + W - 1) / W * 16;
+  const int64_t wb = t0 + w * per_wave;
+  const int64_t we = t1 < wb + per_wave ? t1 : wb + per_wave;  // wave w's tokens: [wb, we)
 
-  // Loads that do not depend on the context length go out together: the
-  // length, this wave's first block-table entries and (decode-only) Q.
-  const int64_t L_raw = load_index(p.seq_lens, s, p.sl64);
-  const int64_t tb0 = t_split0 + w * CH;
-  int64_t blk[NT];
-#pragma unroll
-  for (int j = 0; j < NT; ++j) {
-    // Clamped into the table so the load is unconditional; entries past the
-    // split are never used.
-    int64_t t = tb0 + 16 * j + c16;
-    t = t < t_cap ? t : t_cap - 1;
-    t = t > 0 ? t : 0;
-    blk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
-  }
-  int64_t qtok = s;
-  if (!p.decode_only) {
-    const int64_t q0 = load_index(p.qsl, s, p.qsl64);
-    const int64_t q1 = load_index(p.qsl, s + 1, p.qsl64);
-    if (q1 - q0 != 1) return;  // not a decode row: the varlen kernel owns it
-    qtok = q0;
-  }
-  if (qtok < 0 || qtok >= p.num_tokens) return;
   V8 qop[NC];
   {
     const int hq = c16 < G ? c16 : G - 1;  // in-row address for the padding columns
@@ -286,27 +274,10 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
       for (int c = 0; c < NC; ++c) qop[c] = zero8<DT>();
   }
-
-  const int64_t L = L_raw < p.max_ctx ? L_raw : p.max_ctx;
   T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
-  const int nsplit_len = static_cast<int>((L + split_tok - 1) / split_tok);
-  // The splits that arrive at this pair's merge.  A plan fixes them from the
-  // host lengths, so every launched workgroup arrives even if the device
-  // length is shorter; a device length the plan does not cover is a broken
-  // contract and poisons the pair with NaN.
-  int bad = 0;
-  int nsplit = nsplit_len;
-  if (p.plan_n > 0) {
-    bad = nsplit_len > nsplit_plan;
-    nsplit = nsplit_plan;
-  } else if (split >= nsplit_len) {
-    if (split == 0)  // no key is visible: the reference's masked softmax yields zeros
-      for (int i = tid; i < G * D; i += THREADS) out_row[i] = static_cast<T>(0.f);
-    return;
-  }
-  const int64_t t_split1 = L < t_split0 + split_tok ? L : t_split0 + split_tok;
 
   T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
+  int bad = 0;
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NN];
 #pragma unroll
@@ -314,68 +285,108 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between slots
   const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
   const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
+  const T* zbase = reinterpret_cast<const T*>(p.zeros) + 8 * g;  // a never-written zero page
 
-  // Issue the K/V loads of the step starting at token tb: returns, per
-  // 16-token tile, whether this lane's token is valid (its V is zeroed at
-  // use, so nothing here waits for the data).  Invalid lanes read slot 0,
-  // which is always in bounds.
+  // Issue the K/V loads of the step starting at token tb.  Lanes past the
+  // wave's range or with an invalid block id read the zero page, so their V
+  // contributes nothing (their scores are masked) and nothing here or later
+  // waits on the data to fix it up.
   auto issue_step = [&](int64_t tb, const int64_t (&bk)[NT], V8 (&kx)[NT][NC], V8 (&vx)[NT][NC]) {
-    int vmask = 0;
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int64_t t = tb + 16 * j + c16;
-      bool valid = t < t_split1;
+      bool valid = t < we;
       if (valid && (bk[j] < 0 || bk[j] >= p.num_blocks)) {
         bad = 1;
         valid = false;
       }
-      const int64_t off = valid ? ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride : 0;
+      const int64_t off = ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride;
+      const T* kp = valid ? kbase + off : zbase;
+      const T* vp = valid ? vbase + off : zbase;
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
-        kx[j][c] = load16<DT>(kbase + off + 32 * c);
-        vx[j][c] = load16<DT>(vbase + off + 32 * c);
+        kx[j][c] = load16<DT>(kp + 32 * c);
+        vx[j][c] = load16<DT>(vp + 32 * c);
       }
-      vmask |= valid ? 1 << j : 0;
-    }
-    return vmask;
-  };
-  // Block-table entries of the step at tb (clamped into this split).
-  auto table_step = [&](int64_t tb, int64_t (&bk)[NT]) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      int64_t t = tb + 16 * j + c16;
-      t = t < t_split1 ? t : t_split1 - 1;
-      bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
     }
   };
 
-  // Software pipeline over the wave's steps: step i+1's K/V loads and step
-  // i+2's table entries are in flight while step i computes.
-  V8 kr[NT][NC], vr[NT][NC];
-  int vmask = 0;
-  if (tb0 < t_split1) {
-    vmask = issue_step(tb0, blk, kr, vr);
-    table_step(tb0 + W * CH, blk);
+  // Where the block ids of every step come from.  BIG (block size >= 16: a
+  // tile lies in one block): the item carries those of the wave's first IS
+  // steps, and the ids of its later tiles come in one vector load (lane l:
+  // tile IS * NT + l) issued before any K/V load and staged in LDS, so the
+  // step loop reads them with LDS loads.  Vector-memory loads return in
+  // order, and this way no K/V load waits for another step's data.  (The
+  // plan caps an item at 4096 tokens, which keeps a wave within IS * NT + 64
+  // tiles.)  Smaller blocks: per-lane block-table entries per step, clamped
+  // into the wave's range.
+  const int64_t nsteps = wb < we ? (we - wb + CH - 1) / CH : 0;
+  // Loads in the BIG kernel are unconditional (clamped addresses, or the
+  // zero page), so the compiler can count them exactly: a wait for one step's
+  // data never turns into a wait for everything in flight.
+  int64_t later_ids = 0;
+  if constexpr (BIG) {
+    int64_t t = wb + 16 * (IS * NT + lane);
+    t = t < we ? t : we - 1;
+    t = t > 0 ? t : 0;
+    later_ids = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
   }
-  for (int64_t tb = tb0; tb < t_split1; tb += W * CH) {
-    if (!PIPE && tb != tb0) {
-      // Without the pipeline (one step per wave in the common case) later
-      // steps issue their loads at the top of the step.
-      vmask = issue_step(tb, blk, kr, vr);
-      table_step(tb + W * CH, blk);
+  int64_t* my_later = later_lds + w * 64;
+  auto step_blocks = [&](int64_t st, int64_t (&bk)[NT]) {
+    if constexpr (BIG) {
+      if (st < IS) {
+#pragma unroll
+        for (int q = 0; q < IS; ++q)
+          if (q == st)
+#pragma unroll
+            for (int j = 0; j < NT; ++j) bk[j] = ib.id[q * NT + j];
+      } else {
+        const int64_t* src = my_later + (st - IS) * NT;
+#pragma unroll
+        for (int j = 0; j < NT; ++j) bk[j] = src[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        int64_t t = wb + st * CH + 16 * j + c16;
+        t = t < we ? t : we - 1;
+        t = t > 0 ? t : 0;
+        bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+      }
     }
-    const bool has_next = PIPE && tb + W * CH < t_split1;
+  };
+
+  // Software pipeline over the wave's steps: step st + 1's K/V loads are in
+  // flight while step st computes.
+  V8 kr[NT][NC], vr[NT][NC];
+  if (BIG || nsteps > 0) {
+    int64_t bk[NT];
+    step_blocks(0, bk);
+    issue_step(wb, bk, kr, vr);
+  }
+  if constexpr (BIG) {
+    my_later[lane] = later_ids;  // waits for the id load only: it went out before the K/V loads
+    wave_lds_sync();
+  }
+  for (int64_t st = 0; st < nsteps; ++st) {
+    const int64_t tb = wb + st * CH;
+    const bool has_next = st + 1 < nsteps;
     V8 kn[NT][NC], vn[NT][NC];
-    int vmask_n = 0;
-    if (has_next) {
-      vmask_n = issue_step(tb + W * CH, blk, kn, vn);
-      table_step(tb + 2 * W * CH, blk);
+    if (BIG || has_next) {
+      // (BIG: past the wave's last step every lane reads the zero page.)
+      int64_t bk[NT];
+      step_blocks(has_next ? st + 1 : st, bk);
+      issue_step(tb + CH, bk, kn, vn);
     }
+    // Scheduling boundary: the next step's loads are issued before anything
+    // below uses (and so waits for) this step's K/V registers.  The empty asm
+    // takes them as in/out operands, so nothing that reads them can be
+    // hoisted above it, and its memory clobber keeps the loads above it.
+    asm volatile("" ::: "memory");
 #pragma unroll
     for (int j = 0; j < NT; ++j)
-      if (!(vmask >> j & 1))
 #pragma unroll
-        for (int c = 0; c < NC; ++c) vr[j][c] = zero8<DT>();
+      for (int c = 0; c < NC; ++c) asm volatile("" : "+v"(kr[j][c]), "+v"(vr[j][c]));
     // Stage V transposed (vt[dim][token]) for the PV operand.
 #pragma unroll
     for (int j = 0; j < NT; ++j)
@@ -399,7 +410,7 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t t = tb + 16 * j + 4 * g + r;
-        const float x = t < t_split1 ? sacc[j][r] * p.scale_log2 : -INFINITY;
+        const float x = t < we ? sacc[j][r] * p.scale_log2 : -INFINITY;
         sv[j][r] = x;
         mloc = fmaxf(mloc, x);
       }
@@ -434,9 +445,9 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
       }
 #pragma unroll
       for (int n = 0; n < NN; ++n) {
-        const T* r0 = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0 + 16);
+        const T* r0p = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0p);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0p + 16);
         const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
         acc[n] = mfma16x16x32(DT{}, va, pt, acc[n]);
       }
@@ -450,7 +461,6 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
           kr[j][c] = kn[j][c];
           vr[j][c] = vn[j][c];
         }
-      vmask = vmask_n;
     }
   }
   l_run = group4_sum(l_run);
@@ -473,9 +483,10 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   }
   __syncthreads();
 
-  // One float4 of the workgroup's output per thread: (head col, dims 4*d4..+3).
-  const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
-  const PartBuffers pbuf = part_buffers(p);
+  const int slot_words = p.slot_words;
+  const __amdgpu_buffer_rsrc_t pr =
+      __builtin_amdgcn_make_buffer_rsrc(p.part, static_cast<short>(0), p.part_bytes, kBufferWord3);
+  // One float4 of the workgroup's output per thread and round: (head col, dims 4*d4..+3).
   for (int it = tid; it < G * (D / 4); it += THREADS) {
     const int col = it / (D / 4), d4 = it % (D / 4);
     float M = -INFINITY;
@@ -503,27 +514,49 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
       for (int r = 0; r < 4; ++r) v4[r] = static_cast<T>(o[r] * inv);
       *reinterpret_cast<u32x2*>(out_row + col * D + 4 * d4) = __builtin_bit_cast(u32x2, v4);
     } else {
-      const int pi = static_cast<int>((pair * p.max_splits + split) * G + col);
-      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), pbuf.o, pi * (D * 4) + 16 * d4, 0, kSc1);
+      const int base = static_cast<int>(idx) * slot_words;
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, o), pr, 4 * (base + col * D + 4 * d4), 0,
+                                             kSc1);
       if (d4 == 0)
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__builtin_bit_cast(uint32_t, M), __builtin_bit_cast(uint32_t, lsum)},
-                                              pbuf.ml, pi * 8, 0, kSc1);
+        __builtin_amdgcn_raw_buffer_store_b64(
+            u32x2{__builtin_bit_cast(uint32_t, M), __builtin_bit_cast(uint32_t, lsum)}, pr,
+            4 * (base + G * D + 2 * col), 0, kSc1);
     }
   }
   if (nsplit == 1) return;
 
-  // Split-K merge inside the same launch: the last workgroup of this pair to
-  // arrive combines every split's partial.
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's partial stores are acknowledged
+  // Arrive only once this workgroup's partial is acknowledged (device scope).
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
   if (tid == 0) {
     const unsigned prev = __hip_atomic_fetch_add(&p.counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == static_cast<unsigned>(nsplit - 1);
+    s_merger = prev == static_cast<unsigned>(nsplit - 1);
   }
   __syncthreads();
-  if (!s_last) return;
-  merge_splits<DT, D, THREADS>(p, pbuf, pair, nsplit, out_row);
+  if (!s_merger) return;
+  merge_partials<DT, D, THREADS>(p, pr, first, nsplit, out_row);
   if (tid == 0) __hip_atomic_store(&p.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <class DT, int D, int W, int CH, class BTI, bool BIG>
+__global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) char smem[DecodeCfg<D, W, CH>::LDS];
+  __shared__ int64_t later_lds[BIG ? W * 64 : 1];
+  __shared__ int s_merger;
+  // The first item loads together with the plan's item count: the grid
+  // never exceeds the plan's capacity, so the read is in bounds either way.
+  uint32_t idx = blockIdx.x;
+  u32x4 r0, r1;
+  WaveBlocks<W, CH> ib;
+  load_item<W, CH>(p, idx, r0, r1, ib);
+  const uint32_t n_hdr = p.plan_hdr->n_items;
+  const uint32_t n_items = n_hdr < p.item_cap ? n_hdr : static_cast<uint32_t>(p.item_cap);
+  while (idx < n_items) {
+    decode_item<DT, D, W, CH, BTI, BIG>(p, idx, r0, r1, ib, smem, later_lds, s_merger);
+    idx += gridDim.x;
+    if (idx < n_items) load_item<W, CH>(p, idx, r0, r1, ib);
+    __syncthreads();  // the next item reuses the LDS
+  }
 }
 
 // --------------------------------------------------------------------------
@@ -1031,6 +1064,13 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
             const int on = uofs(slot0 + k, ct, 1 + n);
             ak[n] = floatx4{ld_sc1(pr, on), ld_sc1(pr, on + 4), ld_sc1(pr, on + 8), ld_sc1(pr, on + 12)};
           }
+          // The slot units this lane read are its own (every split stored
+          // them at the same wave, tile and lane): clear them for the next
+          // call, whose workspace tail must be zero.
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, pr, o0, 0, kSc1);
+#pragma unroll
+          for (int n = 0; n < NN; ++n)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, pr, uofs(slot0 + k, ct, 1 + n), 0, kSc1);
           bad_out |= lk != lk;
           const float a = mx[ct] == -INFINITY ? 0.f : fast_exp2(mk - mx[ct]);
           l_run[ct] += lk * a;
@@ -1062,11 +1102,6 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnPara
 // --------------------------------------------------------------------------
 // Host side.
 // --------------------------------------------------------------------------
-struct DecodePlan {
-  int split_tokens;
-  int max_splits;
-};
-
 // 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
 constexpr int kPrefillTiles = 2;
 
@@ -1076,22 +1111,16 @@ constexpr int kDecodeWaves = 4;
 template <int D>
 constexpr int decode_chunk() { return D == 64 ? 64 : 32; }
 
-// Tokens per decode workgroup: one step of every wave, doubled until a
-// sequence needs at most 64 workgroups, which bounds the partial buffers
-// while giving short batches enough workgroups to cover 256 CUs.
-DecodePlan plan_decode(int head_dim, int64_t ctx_tokens) {
-  const int base = kDecodeWaves * (head_dim == 64 ? decode_chunk<64>() : decode_chunk<128>());
-  int64_t tok = base;
-  while ((ctx_tokens + tok - 1) / tok > 64) tok *= 2;
-  DecodePlan plan;
-  plan.split_tokens = static_cast<int>(tok);
-  plan.max_splits = static_cast<int>(ctx_tokens <= 0 ? 1 : (ctx_tokens + tok - 1) / tok);
-  return plan;
-}
+// Words of one decode split-K slot: G rows of D outputs, then G (max, sum)
+// pairs, padded to 16 bytes.
+int slot_words(int group, int head_dim) { return (group * head_dim + 2 * group + 3) / 4 * 4; }
 
 struct WorkspaceLayout {
-  size_t counters_off, ml_off, o_off;
-  size_t pf_counters_off, pf_part_off, pf_part_bytes;  // prefill split-K region (0 bytes: none)
+  size_t counters_off, pf_counters_off;  // arrival counters (zero between calls)
+  size_t zero_off;                       // a page no call writes (zero since the workspace was cleared)
+  size_t plan_off, plan_cap;             // the call's own decode plan, when the caller passes none
+  size_t pf_part_off, pf_part_bytes;     // prefill split-K slots (zero between calls; 0 bytes: none)
+  size_t part_off, part_bytes;           // decode split-K slots (hold the last call's partials)
   size_t total;
 };
 
@@ -1101,29 +1130,95 @@ constexpr int kPrefillSlots = 512;
 size_t prefill_slot_bytes(int head_dim) {
   return head_dim == 64 ? PrefillCfg<64, kPrefillTiles>::SLOT_BYTES : PrefillCfg<128, kPrefillTiles>::SLOT_BYTES;
 }
+constexpr size_t kPrefillRegion =
+    size_t{kPrefillSlots} * (PrefillCfg<64, kPrefillTiles>::SLOT_BYTES > PrefillCfg<128, kPrefillTiles>::SLOT_BYTES
+                                 ? PrefillCfg<64, kPrefillTiles>::SLOT_BYTES
+                                 : PrefillCfg<128, kPrefillTiles>::SLOT_BYTES);
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// Arrival counters sit at the same offsets for every call (decode pairs from
-// 0, prefill pairs after kMaxDecodePairs), ahead of all partials: a workspace
-// reused by calls of other shapes never has one call's partials where another
-// call's counters are, so the counters stay at zero between calls.
+// Everything but the decode split-K slots sits at the same offsets for every
+// call: the arrival counters (decode pairs from 0, prefill pairs after
+// kMaxDecodePairs), a zero page, the region the call's own decode plan is
+// built in and, for calls with prefill rows, the prefill split-K slots
+// (sized for the largest head_dim).  The counters and the prefill slots are
+// zero between calls -- their protocols need that, and the workgroup that
+// consumes a prefill slot clears it -- so a workspace reused by calls of
+// other shapes never shows one call's data to another.  Decode slots come
+// last and need no clearing: a merger reads only slots its own call's
+// producers wrote and acknowledged before they arrived.
 constexpr size_t kMaxDecodePairs = (size_t{1} << 20) - kPrefillSlots;
 constexpr size_t kCounterBytes = (kMaxDecodePairs + kPrefillSlots) * sizeof(unsigned);
+constexpr size_t kZeroPageBytes = 4096;  // read by decode lanes that have no token to load
+constexpr size_t kPlanRegion = (size_t{4} << 20) - kZeroPageBytes;
 
-WorkspaceLayout workspace_layout(int num_seqs, int num_kv_heads, int group, int head_dim,
-                                 const DecodePlan& plan, bool with_prefill) {
-  const size_t pairs = static_cast<size_t>(num_seqs) * num_kv_heads;
-  const size_t parts = pairs * plan.max_splits * group;
+WorkspaceLayout workspace_layout(int group, int head_dim, int64_t item_cap, bool with_prefill) {
   WorkspaceLayout l;
   l.counters_off = 0;
   l.pf_counters_off = kMaxDecodePairs * sizeof(unsigned);
-  l.ml_off = kCounterBytes;
-  l.o_off = align_up(l.ml_off + parts * 2 * sizeof(float), 256);
-  l.pf_part_off = align_up(l.o_off + parts * head_dim * sizeof(float), 256);
+  l.zero_off = kCounterBytes;
+  l.plan_off = l.zero_off + kZeroPageBytes;
+  l.plan_cap = kPlanRegion;
+  l.pf_part_off = l.plan_off + l.plan_cap;
   l.pf_part_bytes = with_prefill ? kPrefillSlots * prefill_slot_bytes(head_dim) : 0;
-  l.total = align_up(l.pf_part_off + l.pf_part_bytes, 256);
+  l.part_off = l.pf_part_off + kPrefillRegion;
+  l.part_bytes = align_up(static_cast<size_t>(item_cap) * slot_words(group, head_dim) * 4, 256);
+  l.total = align_up(l.part_off + l.part_bytes, 256);
   return l;
+}
+
+// Decode grid and plan capacity of a call: CUs x rounds workgroups loop over
+// the plan's items, which never exceed kPlanCUs x rounds + num_seqs x Hkv.
+struct DecodeShape {
+  int rounds;
+  int64_t item_cap;
+  int cus, grid;
+};
+
+DecodeShape decode_shape(int num_seqs, int num_kv_heads, int64_t max_ctx, int head_dim, int device_cus) {
+  DecodeShape d;
+  d.rounds = plan_max_rounds(num_seqs, num_kv_heads, max_ctx, head_dim);
+  d.item_cap = plan_item_cap(num_seqs, num_kv_heads, max_ctx, d.rounds);
+  d.cus = device_cus < 1 ? 1 : (device_cus > kPlanCUs ? kPlanCUs : device_cus);
+  d.grid = d.cus * d.rounds;
+  return d;
+}
+
+size_t plan_bytes_needed(int64_t num_seqs, int64_t item_cap) { return plan_bytes(num_seqs, item_cap); }
+
+int current_device_cus() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) !=
+                                              hipSuccess)
+    return kPlanCUs;
+  return n;
+}
+
+DecodePlanArgs plan_args(void* plan, int64_t item_cap, const void* block_tables, int64_t bt_stride, int bt64,
+                         int bs_shift, const void* seq_lens, int sl64, const void* qsl, int qsl64,
+                         int is_decode_only, int num_seqs, int num_kv_heads, int64_t max_ctx, int head_dim,
+                         const DecodeShape& d) {
+  DecodePlanArgs a;
+  a.plan = plan;
+  a.item_cap = static_cast<uint32_t>(item_cap);
+  a.block_tables = block_tables;
+  a.bt_stride = bt_stride;
+  a.bt64 = bt64 ? 1 : 0;
+  a.bs_shift = bs_shift;
+  a.tiles_per_step = (head_dim == 64 ? decode_chunk<64>() : decode_chunk<128>()) / 16;
+  a.seq_lens = seq_lens;
+  a.sl64 = sl64 ? 1 : 0;
+  a.qsl = qsl;
+  a.qsl64 = qsl64 ? 1 : 0;
+  a.decode_only = is_decode_only ? 1 : 0;
+  a.num_seqs = num_seqs;
+  a.num_kv_heads = num_kv_heads;
+  a.max_ctx = max_ctx;
+  a.cus = d.cus;
+  a.rounds = d.rounds;
+  a.min_tokens = plan_min_tokens(head_dim);
+  a.round_tokens = plan_round_tokens(head_dim);
+  return a;
 }
 
 int ilog2_exact(int v) {
@@ -1153,26 +1248,44 @@ struct AuxStream {
 // compute-bound prefill kernel; graph capture records the fork and join as
 // ordinary cross-stream dependencies.  Without one the two launches run in
 // order on `stream`.
+// The decode rows: the plan kernel first when the call builds its own plan
+// (`build` non-null), then the decode kernel over `grid` workgroups.
 template <class DT, int D>
-hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool launch_decode, int num_seqs,
-                            int max_query_len, hipStream_t stream, const AuxStream* aux) {
+hipError_t launch_decode_rows(AttnParams& p, const DecodePlanArgs* build, int grid, hipStream_t stream) {
+  if (build) {
+    const hipError_t e = launch_decode_plan(*build, stream);
+    if (e != hipSuccess) return e;
+  }
   void* args[] = {&p};
-  void* pargs[] = {&pp};
   constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
   // The block-table width is a template argument so table loads need no
   // per-lane branch.
-  // Workgroups whose waves take several steps pipeline their K/V loads
-  // (double-buffered registers, fewer resident waves); one-step workgroups
-  // keep the lean variant and its occupancy.
-  const bool pipe = p.split_tokens_max > W * CH;
+  // Block size >= 16 (the item carries block ids) and the table's index
+  // width select the kernel at compile time.
   const void* dk =
-      p.bt64 ? (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, true>)
-                     : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, false>))
-             : (pipe ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, true>)
-                     : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, false>));
-  const dim3 grid = p.plan_n > 0 ? dim3(p.plan_n, 1, 1) : dim3(p.max_splits, p.num_kv_heads, num_seqs);
-  if (p.decode_only) return hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
+      p.inline_blocks
+          ? (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, true>)
+                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, true>))
+          : (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, false>)
+                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, false>));
+  return hipLaunchKernel(dk, dim3(grid), dim3(W * 64), args, 0, stream);
+}
 
+// Launch the decode rows with `p` and, unless the batch is decode-only, the
+// prefill kernel with `pp` (its own plan); `launch_decode` is false when the
+// host query offsets show no one-row sequence.  A mixed batch with an aux
+// stream runs its decode rows there, forked from and joined back to `stream`
+// with the caller's events, so the memory-bound decode kernel overlaps the
+// compute-bound prefill kernel; graph capture records the fork and join as
+// ordinary cross-stream dependencies.  Without one the launches run in order
+// on `stream`.
+template <class DT, int D>
+hipError_t launch_attention(AttnParams& p, AttnParams& pp, const DecodePlanArgs* build, int decode_grid,
+                            int pf_grid_x, bool launch_decode, int num_seqs, int max_query_len, hipStream_t stream,
+                            const AuxStream* aux) {
+  if (p.decode_only) return launch_decode_rows<DT, D>(p, build, decode_grid, stream);
+
+  void* pargs[] = {&pp};
   using PCfg = PrefillCfg<D, kPrefillTiles>;
   const void* vk = pp.bt64 ? reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int64_t>)
                            : reinterpret_cast<const void*>(&paged_prefill_kernel<DT, D, kPrefillTiles, int32_t>);
@@ -1188,7 +1301,7 @@ hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool l
   if (!launch_decode) return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
 
   if (!aux) {
-    hipError_t e = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, stream);
+    hipError_t e = launch_decode_rows<DT, D>(p, build, decode_grid, stream);
     if (e != hipSuccess) return e;
     return hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
   }
@@ -1197,7 +1310,7 @@ hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool l
   if (e != hipSuccess) return e;
   // Once the aux stream depends on the caller's, it is joined back whatever
   // else fails (an unjoined fork would also break a graph capture).
-  const hipError_t ed = hipLaunchKernel(dk, grid, dim3(W * 64), args, 0, aux->stream);
+  const hipError_t ed = launch_decode_rows<DT, D>(p, build, decode_grid, aux->stream);
   const hipError_t er = hipEventRecord(aux->join, aux->stream);
   const hipError_t ev = hipLaunchKernel(vk, vgrid, dim3(PCfg::THREADS), pargs, 0, stream);
   const hipError_t ej = er == hipSuccess ? hipStreamWaitEvent(stream, aux->join, 0) : er;
@@ -1206,146 +1319,8 @@ hipError_t launch_attention(AttnParams& p, AttnParams& pp, int pf_grid_x, bool l
 
 bool aligned16(const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; }
 
-// Fill p.plan from host-side context lengths: one entry per (sequence, kv
-// head, split) of a decode batch.  Workgroup x runs on XCD x % 8 (the
-// dispatcher's round-robin over XCDs), so the pairs are bin-packed onto the 8
-// XCDs by context length (longest first, each to the least loaded XCD) and a
-// pair's splits all get ids of one residue: its partials then meet in one L2.
-// Within an XCD the longest pairs come first, so their merges overlap the
-// streaming of shorter ones.  Returns the entry count (a multiple of 8,
-// unused slots kPlanEmpty), or 0 when the batch does not fit the plan (the
-// launch then uses the full (max_splits, Hkv, S) grid).
-int build_decode_plan_for(AttnParams& p, const std::vector<std::pair<int64_t, int>>& order, int split) {
-  constexpr int kXcds = 8;
-  int64_t units = 0;
-  for (const auto& pr : order) {
-    const int64_t n = (pr.first + split - 1) / split;
-    units += (n < 1 ? 1 : n) * p.num_kv_heads;
-  }
-  if (units > kPlanMax) return 0;
-  std::vector<uint32_t> bucket[kXcds];
-  int64_t load[kXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (const auto& [L, i] : order) {
-    int64_t n = (L + split - 1) / split;
-    n = n < 1 ? 1 : n;
-    for (int kvh = 0; kvh < p.num_kv_heads; ++kvh) {
-      int b = 0;
-      for (int x = 1; x < kXcds; ++x)
-        if (load[x] < load[b]) b = x;
-      load[b] += L + split / 4;  // tokens, plus a per-pair overhead
-      for (int64_t sp = 0; sp < n; ++sp)
-        bucket[b].push_back(static_cast<uint32_t>(i) | static_cast<uint32_t>(kvh) << 16 |
-                            static_cast<uint32_t>(sp) << 20 | static_cast<uint32_t>(n - 1) << 26);
-    }
-  }
-  size_t rows = 0;
-  for (int x = 0; x < kXcds; ++x) rows = bucket[x].size() > rows ? bucket[x].size() : rows;
-  if (rows * kXcds > static_cast<size_t>(kPlanMax)) return 0;
-  for (size_t k = 0; k < rows; ++k)
-    for (int x = 0; x < kXcds; ++x)
-      p.plan[k * kXcds + x] = k < bucket[x].size() ? bucket[x][k] : kPlanEmpty;
-  p.split_tokens = split;
-  p.split_tokens_max = split;
-  return static_cast<int>(rows * kXcds);
-}
-
-// Pair-list plan at a given split: the same XCD bin-packing as above, but
-// one kernel-argument entry pair per (sequence, kv head) instead of one entry
-// per workgroup, so long contexts keep short splits (the dispatcher then
-// balances the tail) without overflowing the kernel arguments.
-// A pair's split is the base, doubled until the pair has at most
-// kMaxPairSplits splits: the last split to arrive merges them all, and that
-// merge's length grows with their number.
-constexpr int kPairMax = (kPlanMax - 9) / 2;
-constexpr int kMaxPairSplits = 64;
-
-int build_decode_pair_plan(AttnParams& p, const std::vector<std::pair<int64_t, int>>& order, int split) {
-  constexpr int kXcds = 8;
-  if (static_cast<int64_t>(order.size()) * p.num_kv_heads > kPairMax) return 0;
-  struct Item {
-    uint32_t e;
-    int64_t n;
-    int shift;
-  };
-  std::vector<Item> bucket[kXcds];
-  int64_t load[kXcds] = {0, 0, 0, 0, 0, 0, 0, 0};
-  int max_shift = 0;
-  for (const auto& [L, i] : order) {
-    int shift = 0;
-    while ((L + (static_cast<int64_t>(split) << shift) - 1) / (static_cast<int64_t>(split) << shift) > kMaxPairSplits)
-      ++shift;
-    if (shift > 20) return 0;
-    const int64_t sp = static_cast<int64_t>(split) << shift;
-    int64_t n = (L + sp - 1) / sp;
-    n = n < 1 ? 1 : n;
-    max_shift = shift > max_shift ? shift : max_shift;
-    for (int kvh = 0; kvh < p.num_kv_heads; ++kvh) {
-      int b = 0;
-      for (int x = 1; x < kXcds; ++x)
-        if (load[x] < load[b]) b = x;
-      load[b] += L + sp / 4;
-      bucket[b].push_back({static_cast<uint32_t>(i) | static_cast<uint32_t>(kvh) << 16 |
-                               static_cast<uint32_t>(n - 1) << 20,
-                           n, shift});
-    }
-  }
-  int k = 0;
-  int64_t rows = 0;
-  for (int x = 0; x < kXcds; ++x) {
-    p.plan[x] = static_cast<uint32_t>(k);
-    int64_t first = 0;
-    for (const Item& it : bucket[x]) {
-      if (first > 0x3FFFFFF) return 0;
-      p.plan[9 + 2 * k] = it.e;
-      p.plan[10 + 2 * k] = static_cast<uint32_t>(first) | static_cast<uint32_t>(it.shift) << 26;
-      first += it.n;
-      ++k;
-    }
-    rows = first > rows ? first : rows;
-  }
-  p.plan[kXcds] = static_cast<uint32_t>(k);
-  if (rows * kXcds > 0x7FFFFFFF) return 0;
-  p.split_tokens = split;
-  p.split_tokens_max = split << max_shift;
-  p.plan_pairs = k;
-  return static_cast<int>(rows * kXcds);
-}
-
-// The split starts at the workspace layout's (so at most max_splits per
-// sequence).  If one entry per workgroup does not fit, a pair-list plan keeps
-// that split; failing that, the split doubles until the batch fits: long
-// contexts then get long splits, whose waves pipeline their steps.
 int64_t host_index(const void* a, int is64, int64_t i) {
   return is64 ? static_cast<const int64_t*>(a)[i] : static_cast<const int32_t*>(a)[i];
-}
-
-// With host query offsets only the one-row sequences are planned (a batch
-// without any gets an empty plan, -1, and no decode launch).
-int build_decode_plan(AttnParams& p, const void* lens, int lens64, const void* qsl, int qsl64, int num_seqs) {
-  if (num_seqs > 0xFFFF || p.num_kv_heads > 16 || p.max_splits > 64) return 0;
-  std::vector<std::pair<int64_t, int>> order;
-  order.reserve(num_seqs);
-  for (int i = 0; i < num_seqs; ++i) {
-    if (qsl && host_index(qsl, qsl64, i + 1) - host_index(qsl, qsl64, i) != 1) continue;
-    int64_t L = host_index(lens, lens64, i);
-    L = L < 0 ? 0 : (L < p.max_ctx ? L : p.max_ctx);
-    order.push_back({L, i});
-  }
-  if (order.empty()) return -1;
-  std::stable_sort(order.begin(), order.end(),
-                   [](const std::pair<int64_t, int>& a, const std::pair<int64_t, int>& b) { return a.first > b.first; });
-  p.plan_pairs = 0;
-  {
-    const int n = build_decode_plan_for(p, order, p.split_tokens);
-    if (n > 0) return n;
-    const int np = build_decode_pair_plan(p, order, p.split_tokens);
-    if (np > 0) return np;
-  }
-  for (int64_t split = p.split_tokens;; split *= 2) {
-    const int n = build_decode_plan_for(p, order, static_cast<int>(split));
-    if (n > 0) return n;
-    if (split >= p.max_ctx || split > (1 << 24)) return 0;  // one split per sequence did not fit either
-  }
 }
 
 // Fill pp.plan with the prefill schedule from host query offsets and lengths:
@@ -1455,9 +1430,48 @@ extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads,
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads ||
       block_size <= 0 || max_seq_len < 0 || (head_dim != 64 && head_dim != 128))
     return 0;
-  const ns::DecodePlan plan = ns::plan_decode(head_dim, ns::round_up_ctx(max_seq_len, block_size));
-  return ns::workspace_layout(num_seqs, num_kv_heads, num_heads / num_kv_heads, head_dim, plan, !is_decode_only)
-      .total;
+  const ns::DecodeShape d =
+      ns::decode_shape(num_seqs, num_kv_heads, ns::round_up_ctx(max_seq_len, block_size), head_dim, ns::kPlanCUs);
+  return ns::workspace_layout(num_heads / num_kv_heads, head_dim, d.item_cap, !is_decode_only).total;
+}
+
+extern "C" size_t ns_paged_decode_plan_size(int num_seqs, int num_kv_heads, int head_dim, int block_size,
+                                            int max_seq_len) {
+  if (num_seqs <= 0 || num_kv_heads <= 0 || block_size <= 0 || max_seq_len < 0 ||
+      (head_dim != 64 && head_dim != 128))
+    return 0;
+  const ns::DecodeShape d =
+      ns::decode_shape(num_seqs, num_kv_heads, ns::round_up_ctx(max_seq_len, block_size), head_dim, ns::kPlanCUs);
+  return ns::align_up(ns::plan_bytes(num_seqs, d.item_cap), 256);
+}
+
+extern "C" int ns_paged_decode_plan(void* plan, size_t plan_bytes, const void* block_tables,
+                                    int64_t block_table_stride, int64_t block_table_width, int block_tables_is_int64,
+                                    const void* seq_lens, int seq_lens_is_int64, const void* query_start_loc,
+                                    int query_start_loc_is_int64, int num_seqs, int is_decode_only,
+                                    int num_kv_heads, int head_dim, int block_size, int max_seq_len, void* stream) {
+  using namespace ns;
+  if (num_seqs < 0) return NS_ERR_INVALID_ARG;
+  if (num_seqs == 0) return NS_OK;
+  if (!plan || !block_tables || !seq_lens || (!is_decode_only && !query_start_loc)) return NS_ERR_INVALID_ARG;
+  if (num_kv_heads <= 0 || max_seq_len < 0 || block_table_width <= 0 || block_table_stride < block_table_width)
+    return NS_ERR_INVALID_ARG;
+  if (head_dim != 64 && head_dim != 128) return NS_ERR_UNSUPPORTED;
+  const int bs_shift = ilog2_exact(block_size);
+  if (bs_shift < 0) return NS_ERR_UNSUPPORTED;
+  if (num_seqs > 65535 || num_kv_heads > 65535) return NS_ERR_UNSUPPORTED;
+  if (reinterpret_cast<uintptr_t>(plan) % 16 != 0) return NS_ERR_INVALID_ARG;
+  const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
+  const int64_t table_tokens = block_table_width * static_cast<int64_t>(block_size);
+  const int64_t max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
+  DecodeShape d = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, kPlanCUs);
+  if (plan_bytes < plan_bytes_needed(num_seqs, d.item_cap)) return NS_ERR_WORKSPACE;
+  d = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, current_device_cus());
+  const DecodePlanArgs a = plan_args(plan, d.item_cap, block_tables, block_table_stride, block_tables_is_int64,
+                                     bs_shift, seq_lens, seq_lens_is_int64, query_start_loc,
+                                     query_start_loc_is_int64, is_decode_only, num_seqs, num_kv_heads, max_ctx,
+                                     head_dim, d);
+  return launch_decode_plan(a, static_cast<hipStream_t>(stream)) == hipSuccess ? NS_OK : NS_ERR_HIP;
 }
 
 namespace ns {
@@ -1469,7 +1483,7 @@ namespace {
 // until the process ends.  In host code `g_noalloc_scratch` names a host-side
 // stand-in, never the device memory: kernels and fills get the address that
 // hipGetSymbolAddress returns for the current device, kept per device.
-constexpr size_t kNoallocScratchBytes = size_t{64} << 20;
+constexpr size_t kNoallocScratchBytes = size_t{128} << 20;
 __device__ __align__(256) unsigned char g_noalloc_scratch[kNoallocScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -1516,6 +1530,7 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
                           int num_seqs, int64_t num_tokens, int max_query_len, int max_seq_len,
                           int is_decode_only, int num_heads, int num_kv_heads, int head_dim,
                           int block_size, int64_t num_blocks, float scale, int dtype,
+                          const void* decode_plan, size_t decode_plan_bytes,
                           void* workspace, size_t workspace_bytes, bool noalloc, void* stream,
                           void* aux_stream, void* fork_event, void* join_event) {
   if (num_seqs < 0 || num_tokens < 0) return NS_ERR_INVALID_ARG;
@@ -1548,8 +1563,21 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
                       static_cast<hipEvent_t>(join_event)};
 
   const int64_t ctx_plan = round_up_ctx(max_seq_len, block_size);
-  const DecodePlan plan = plan_decode(head_dim, ctx_plan);
-  const WorkspaceLayout wl = workspace_layout(num_seqs, num_kv_heads, group, head_dim, plan, !is_decode_only);
+  const int64_t table_tokens = block_table_width * static_cast<int64_t>(block_size);
+  const int64_t max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
+  // Sizes first (they do not depend on the device); the device's CU count,
+  // which only shapes the grid, is queried once every check has passed.
+  DecodeShape dshape = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, kPlanCUs);
+  const WorkspaceLayout wl = workspace_layout(group, head_dim, dshape.item_cap, !is_decode_only);
+  if (static_cast<size_t>(num_seqs) * num_kv_heads > kMaxDecodePairs) return NS_ERR_UNSUPPORTED;
+  // Partials are addressed through buffer descriptors with 32-bit offsets.
+  if (wl.part_bytes > 0x7FFFFFFFu || wl.pf_part_bytes > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
+  if (decode_plan) {
+    if (reinterpret_cast<uintptr_t>(decode_plan) % 16 != 0) return NS_ERR_INVALID_ARG;
+    if (decode_plan_bytes < plan_bytes_needed(num_seqs, dshape.item_cap)) return NS_ERR_INVALID_ARG;
+  } else if (plan_bytes_needed(num_seqs, dshape.item_cap) > wl.plan_cap) {
+    return NS_ERR_UNSUPPORTED;  // too many pairs for the workspace's plan region: pass a plan
+  }
   if (noalloc) {
     // Shapes whose workspace exceeds the scratch are refused before any HIP call.
     if (wl.total > kNoallocScratchBytes) return NS_ERR_WORKSPACE;
@@ -1558,9 +1586,7 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
     workspace_bytes = kNoallocScratchBytes;
   }
   if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
-  // Partials are addressed through buffer descriptors with 32-bit offsets.
-  if (wl.pf_part_off - wl.o_off > 0x7FFFFFFFu || wl.pf_part_bytes > 0x7FFFFFFFu) return NS_ERR_UNSUPPORTED;
-  if (static_cast<size_t>(num_seqs) * num_kv_heads > kMaxDecodePairs) return NS_ERR_UNSUPPORTED;
+  dshape = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, current_device_cus());
 
   AttnParams p;
   p.out = static_cast<char*>(out);
@@ -1575,40 +1601,49 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
   p.sl64 = seq_lens_is_int64 ? 1 : 0;
   p.qsl64 = query_start_loc_is_int64 ? 1 : 0;
   p.decode_only = is_decode_only ? 1 : 0;
+  p.num_seqs = num_seqs;
   p.num_tokens = num_tokens;
   p.num_heads = num_heads;
   p.num_kv_heads = num_kv_heads;
   p.group = group;
   p.bs_shift = bs_shift;
   p.num_blocks = num_blocks;
-  const int64_t table_tokens = block_table_width * static_cast<int64_t>(block_size);
-  p.max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
+  p.max_ctx = max_ctx;
   p.scale_log2 = scale * 1.4426950408889634f;
-  p.split_tokens = plan.split_tokens;
-  p.split_tokens_max = plan.split_tokens;
-  p.max_splits = plan.max_splits;
   p.skip_decode_rows = 1;
   char* ws = static_cast<char*>(workspace);
+  char* plan_base = decode_plan ? static_cast<char*>(const_cast<void*>(decode_plan)) : ws + wl.plan_off;
+  p.plan_hdr = reinterpret_cast<const DecodePlanHeader*>(plan_base);
+  p.items = reinterpret_cast<const DecodeItem*>(plan_base + sizeof(DecodePlanHeader));
+  p.item_cap = dshape.item_cap;
+  p.inline_blocks = bs_shift >= 4 ? 1 : 0;
+  p.zeros = static_cast<char*>(workspace) + wl.zero_off;
+  p.part = reinterpret_cast<uint32_t*>(ws + wl.part_off);
+  p.part_bytes = static_cast<int>(wl.part_bytes);
+  p.slot_words = slot_words(group, head_dim);
   p.counters = reinterpret_cast<unsigned*>(ws + wl.counters_off);
-  p.part_ml = reinterpret_cast<float*>(ws + wl.ml_off);
-  p.part_o = reinterpret_cast<float*>(ws + wl.o_off);
-  p.part_ml_bytes = static_cast<int>(wl.o_off - wl.ml_off);
-  p.part_o_bytes = static_cast<int>(wl.pf_part_off - wl.o_off);
   p.pf_counters = reinterpret_cast<unsigned*>(ws + wl.pf_counters_off);
   p.pf_part = reinterpret_cast<float*>(ws + wl.pf_part_off);
   p.pf_part_bytes = static_cast<int>(wl.pf_part_bytes);
   p.plan_n = 0;
-  p.plan_pairs = 0;
-  // Decode plan from the host lengths.  Without host query offsets a mixed
-  // batch's plan covers every sequence and the workgroups of sequences with
-  // more than one query row leave at once (the prefill kernel owns them).
+  // The decode plan is built on the device (in the workspace's plan region)
+  // unless the caller passes one built for this metadata.
+  DecodePlanArgs build_args;
+  const DecodePlanArgs* build = nullptr;
+  if (!decode_plan) {
+    build_args = plan_args(plan_base, dshape.item_cap, block_tables, block_table_stride, block_tables_is_int64,
+                           bs_shift, seq_lens, seq_lens_is_int64, query_start_loc, query_start_loc_is_int64,
+                           is_decode_only, num_seqs, num_kv_heads, max_ctx, head_dim, dshape);
+    build = &build_args;
+  }
+  // With host query offsets, a batch without one-row sequences launches no decode rows.
   const void* qsl_host = is_decode_only ? nullptr : query_start_loc_host;
   bool launch_decode = true;
-  if (seq_lens_host) {
-    const int n = build_decode_plan(p, seq_lens_host, seq_lens_host_is_int64, qsl_host,
-                                    query_start_loc_host_is_int64, num_seqs);
-    launch_decode = n >= 0;
-    p.plan_n = n > 0 ? n : 0;
+  if (qsl_host && seq_lens_host) {
+    launch_decode = false;
+    for (int i = 0; i < num_seqs && !launch_decode; ++i)
+      launch_decode = host_index(qsl_host, query_start_loc_host_is_int64, i + 1) -
+                          host_index(qsl_host, query_start_loc_host_is_int64, i) == 1;
   }
   // Prefill plan (split-K over the CUs) from host offsets and lengths.
   AttnParams pp;
@@ -1627,13 +1662,17 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
 
   hipStream_t st = static_cast<hipStream_t>(stream);
   const AuxStream* ax = aux_given ? &aux : nullptr;
+  const int dg = dshape.grid;
   hipError_t e;
   if (dtype == NS_DTYPE_F16)
-    e = head_dim == 64 ? launch_attention<F16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
-                       : launch_attention<F16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
+    e = head_dim == 64
+            ? launch_attention<F16, 64>(p, pp, build, dg, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
+            : launch_attention<F16, 128>(p, pp, build, dg, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
   else
-    e = head_dim == 64 ? launch_attention<BF16, 64>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
-                       : launch_attention<BF16, 128>(p, pp, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax);
+    e = head_dim == 64
+            ? launch_attention<BF16, 64>(p, pp, build, dg, pf_grid_x, launch_decode, num_seqs, max_query_len, st, ax)
+            : launch_attention<BF16, 128>(p, pp, build, dg, pf_grid_x, launch_decode, num_seqs, max_query_len, st,
+                                          ax);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }
 
@@ -1653,6 +1692,7 @@ extern "C" int ns_paged_attention(void* out, const void* query,
                                   int num_heads, int num_kv_heads, int head_dim,
                                   int block_size, int64_t num_blocks,
                                   float scale, int dtype,
+                                  const void* decode_plan, size_t decode_plan_bytes,
                                   void* workspace, size_t workspace_bytes, void* stream,
                                   void* aux_stream, void* fork_event, void* join_event) {
   return ns::paged_attention_entry(out, query, k_cache, v_cache, block_tables, block_table_stride,
@@ -1660,8 +1700,9 @@ extern "C" int ns_paged_attention(void* out, const void* query,
                                    query_start_loc, query_start_loc_is_int64, seq_lens_host,
                                    seq_lens_host_is_int64, query_start_loc_host, query_start_loc_host_is_int64,
                                    num_seqs, num_tokens, max_query_len, max_seq_len, is_decode_only, num_heads,
-                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, workspace,
-                                   workspace_bytes, false, stream, aux_stream, fork_event, join_event);
+                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, decode_plan,
+                                   decode_plan_bytes, workspace, workspace_bytes, false, stream, aux_stream,
+                                   fork_event, join_event);
 }
 
 extern "C" int ns_paged_attention_noalloc(void* out, const void* query,
@@ -1676,13 +1717,15 @@ extern "C" int ns_paged_attention_noalloc(void* out, const void* query,
                                           int is_decode_only,
                                           int num_heads, int num_kv_heads, int head_dim,
                                           int block_size, int64_t num_blocks,
-                                          float scale, int dtype, void* stream,
+                                          float scale, int dtype,
+                                          const void* decode_plan, size_t decode_plan_bytes, void* stream,
                                           void* aux_stream, void* fork_event, void* join_event) {
   return ns::paged_attention_entry(out, query, k_cache, v_cache, block_tables, block_table_stride,
                                    block_table_width, block_tables_is_int64, seq_lens, seq_lens_is_int64,
                                    query_start_loc, query_start_loc_is_int64, seq_lens_host,
                                    seq_lens_host_is_int64, query_start_loc_host, query_start_loc_host_is_int64,
                                    num_seqs, num_tokens, max_query_len, max_seq_len, is_decode_only, num_heads,
-                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, nullptr, 0,
-                                   true, stream, aux_stream, fork_event, join_event);
+                                   num_kv_heads, head_dim, block_size, num_blocks, scale, dtype, decode_plan,
+                                   decode_plan_bytes, nullptr, 0, true, stream, aux_stream, fork_event,
+                                   join_event);
 }

@@ -127,13 +127,11 @@ class DecodeGraphs:
     the greedy tokens in a static output.  Batches are padded to the bucket
     with slot -1 (the cache write skips it) and length 1.
 
-    Attention inside the graph gets no host lengths, so it runs its full-grid
-    decode: splits sized for the graph's context bound, empty splits exiting
-    at once.  Graphs are therefore also keyed by a context bucket (powers of
-    two up to max_model_len): sizing the grid for 4096 tokens when the batch's
-    longest context is under 1024 doubles the attention time (MI355X, 32
-    sequences: 18.9 us against 9.5 us).  Each graph's block table has its
-    context bucket's width.
+    The forward builds the step's decode plan on the device from the replayed
+    lengths (attn_fn.prepare, once per step), so attention inside the graph is
+    scheduled from the step's actual lengths.  Graphs are also keyed by a
+    context bucket (powers of two up to max_model_len), which sets the width
+    of the graph's block table and so the bytes the fill copies.
 
     `launch` and `tokens` split a step so that the engine can plan and launch
     the next step before reading this one's tokens back: the next step's input

@@ -212,8 +212,13 @@ class Qwen2Model(nn.Module):
         hidden = self.embed_tokens(input_ids)
         if self.rotary.cos_cached.device != positions.device:
             self.rotary.to(positions.device)  # float32 tables follow the model's device
-        # One cos/sin lookup for all layers (qwen2.py:105-113).
+        # One cos/sin lookup for all layers (qwen2.py:105-113), and the
+        # attention backend's per-step preparation (the HIP backend's decode
+        # plan), also shared by all layers.
         cos, sin = self.rotary.cos_sin(positions, hidden.dtype)
+        prepare = getattr(attn_fn, "prepare", None)
+        if prepare is not None:
+            prepare(md, kv_cache.k_cache[0])
         for layer in self.layers:
             hidden = layer(hidden, cos, sin, kv_cache, md, attn_fn)
         return self.norm(hidden)

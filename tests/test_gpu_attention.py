@@ -17,6 +17,7 @@ import pytest
 import torch
 
 from nanoserve_amd import paged_attention_hip
+from nanoserve_amd.attention import _workspaces, prepare_decode_plan
 from nanoserve_amd.workloads import make_case, metadata_for
 from oracle.paged_attention import dense_reference, paged_attention_ref
 from tests._helpers import build_paged, make_md, md_to
@@ -151,62 +152,76 @@ def test_decode_wider_table_and_larger_max_seq_len():
     _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
-def test_decode_plan_and_full_grid_agree_bitwise():
-    """With seq_lens_cpu the library launches one workgroup per split (longest
-    first); without it the grid is sized by max_seq_len.  Same arithmetic, same
-    merge order: identical bits."""
+def test_decode_prepared_plan_and_per_call_plan_agree_bitwise():
+    """The decode plan is built on the device from seq_lens, once per step
+    (prepare_decode_plan) or by each call; with or without the host copies of
+    the lengths the same plan, arithmetic and merge order give identical bits."""
     seqs = [5, 300, 4000, 77, 1, 2048, 0]
     q, kc, vc, md, tables, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16)
     md_nolist = make_md(seqs, [1] * len(seqs), tables, 16, with_cpu_lists=False)
     a = _run(q, kc, vc, md, 0.125)
     b = _run(q, kc, vc, md_nolist, 0.125)
-    assert torch.equal(a, b)
+    mdd = md_to(md, DEV)
+    prepare_decode_plan(mdd, kc.to(DEV))
+    assert mdd.decode_plan is not None
+    c = paged_attention_hip(q.to(DEV), kc.to(DEV), vc.to(DEV), mdd, 0.125).float().cpu()
+    assert torch.equal(a, b) and torch.equal(a, c)
     _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
-def test_decode_plan_long_splits_pipeline_steps():
-    """100 x ~2000 tokens do not fit the plan at 256-token splits; the plan
-    doubles the split until they do, and the waves then pipeline several steps."""
+def test_decode_plan_is_shared_by_the_layers_of_a_step():
+    """One plan, several layers (each its own caches and queries): every call
+    equals the same call planning for itself, and a plan built for other sizes
+    is not used."""
+    seqs = [700, 33, 1900, 260]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * 4, 14, 2, 64, 16, torch.float16)
+    mdd = md_to(md, DEV)
+    prepare_decode_plan(mdd, kc.to(DEV))
+    for layer in range(3):
+        g = torch.Generator().manual_seed(40 + layer)
+        ql = torch.randn(q.shape, generator=g).half().to(DEV)
+        kl = torch.randn(kc.shape, generator=g).half().to(DEV)
+        vl = torch.randn(vc.shape, generator=g).half().to(DEV)
+        shared = paged_attention_hip(ql, kl, vl, mdd, 0.125)
+        own = paged_attention_hip(ql, kl, vl, md_to(md, DEV), 0.125)
+        torch.cuda.synchronize()
+        assert torch.equal(shared, own), f"layer {layer}"
+    # A plan for another head size does not apply to this call: it plans for itself.
+    other = md_to(md, DEV)
+    prepare_decode_plan(other, torch.empty(1, 16, 2, 128, device=DEV, dtype=torch.float16))
+    got = _run(q, kc, vc, other, 0.125)
+    _assert_close(got, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+
+
+def test_decode_many_items_per_pair_and_rounds():
+    """100 x ~2000 tokens: several rounds of items, each pair cut into several
+    items merged in-launch; the waves pipeline several steps per item."""
     seqs = [2000 + 7 * i for i in range(100)]
     q, kc, vc, md, tables, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=3)
     got = _run(q, kc, vc, md, 0.125)
     _assert_close(got, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
-    nolist = make_md(seqs, [1] * len(seqs), tables, 16, with_cpu_lists=False)
-    _assert_close(_run(q, kc, vc, nolist, 0.125), got, torch.float16)
 
 
-def test_decode_plan_overflow_falls_back_to_full_grid():
-    """More (sequence, kv head) pairs than the plan holds: the full grid runs."""
-    seqs = [37 + (7 * i) % 500 for i in range(400)]  # 800 pairs > 768 plan entries
+def test_decode_more_pairs_than_items_per_round():
+    """More (sequence, kv head) pairs than a round of items: one item per pair,
+    the workgroups loop over them."""
+    seqs = [37 + (7 * i) % 500 for i in range(400)]  # 800 pairs
     q, kc, vc, md, _, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16, q_seed=4)
     _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
-def test_decode_host_lengths_shorter_than_device_poison_only_that_sequence():
-    """A device length the host plan does not cover is a broken contract: that
-    sequence's rows are NaN, the others are right, and the split-K counters are
-    left clean for the next call."""
+def test_decode_follows_the_device_lengths_whatever_the_host_copy_says():
+    """Decode rows are planned from the device lengths: a host copy that
+    disagrees (shorter or longer) changes nothing."""
     seqs = [300, 1000, 50]
     q, kc, vc, md, tables, _ = _case(seqs, [1] * 3, 14, 2, 64, 16, torch.float16)
     ref = paged_attention_ref(q, kc, vc, md, 0.125)
-    bad = make_md(seqs, [1] * 3, tables, 16)
-    bad.seq_lens_cpu = [300, 600, 50]
-    got = _run(q, kc, vc, bad, 0.125)
-    assert torch.isnan(got[1]).all()
-    _assert_close(got[[0, 2]], ref[[0, 2]], torch.float16)
-    _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
-    _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
-
-
-def test_decode_host_lengths_longer_than_device_follow_the_device():
-    """Extra planned splits past the device length contribute nothing."""
-    seqs = [300, 1000, 50]
-    q, kc, vc, md, tables, _ = _case(seqs, [1] * 3, 14, 2, 64, 16, torch.float16)
-    ref = paged_attention_ref(q, kc, vc, md, 0.125)
+    shorter = make_md(seqs, [1] * 3, tables, 16)
+    shorter.seq_lens_cpu = [300, 600, 50]
+    _assert_close(_run(q, kc, vc, shorter, 0.125), ref, torch.float16)
     longer = make_md([300, 1500, 50], [1] * 3, [t + [0] * 40 for t in tables], 16)
     longer.seq_lens = md.seq_lens
-    got = _run(q, kc, vc, longer, 0.125)
-    _assert_close(got, ref, torch.float16)
+    _assert_close(_run(q, kc, vc, longer, 0.125), ref, torch.float16)
     _assert_close(_run(q, kc, vc, md, 0.125), ref, torch.float16)
 
 
@@ -433,3 +448,23 @@ def test_rejects_unsupported_shapes():
         paged_attention_hip(torch.zeros(1, 32, 64, device=DEV, dtype=torch.float16), kc, kc, md, 0.1)
     with pytest.raises(TypeError):
         paged_attention_hip(torch.zeros(1, 2, 64, device=DEV), kc.float(), kc.float(), md, 0.1)
+
+
+def test_workspace_counters_and_prefill_slots_are_left_zero():
+    """The arrival counters (the first 4 MiB) and the prefill split-K slots
+    (the 36 MiB after the 8 MiB head) go back to zero after decode calls with
+    merged splits and after a mixed call whose prefill rows split, so a
+    workspace reused by calls of other shapes starts every protocol clean;
+    only the decode slots after them keep partials."""
+    cases = [([4000, 900, 35, 2000, 1], None), ([4000, 900, 35], [300, 900, 1]), ([5000, 64], [64, 64])]
+    head, prefill = 8 << 20, 36 << 20
+    for seqs, qls in cases:
+        qls = qls or [1] * len(seqs)
+        q, kc, vc, md, _, _ = _case(seqs, qls, 14, 2, 64, 16, torch.float16)
+        _assert_close(_run(q, kc, vc, md, 0.125), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+        stream = torch.cuda.current_stream().cuda_stream
+        ws = _workspaces[(torch.cuda.current_device(), stream)]
+        torch.cuda.synchronize()
+        assert ws.numel() >= head + prefill
+        assert not ws[:4 << 20].any(), "arrival counters must be back at zero"
+        assert not ws[head:head + prefill].any(), f"{len(seqs)} seqs: prefill split slots not cleared"

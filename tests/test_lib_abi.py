@@ -47,7 +47,7 @@ def test_status_strings_and_version():
 def _attn_args(**over):
     a = dict(out=16, query=16, k_cache=16, v_cache=16, bt=16, bt_stride=4, bt_width=4, bt64=0,
              sl=16, sl64=0, qsl=16, qsl64=0, slh=None, slh64=0, qslh=None, qslh64=0, S=2, T=2, maxq=1, maxs=64, decode_only=1,
-             Hq=14, Hkv=2, D=64, bs=16, nb=32, scale=0.125, dtype=_lib.NS_DTYPE_F16,
+             Hq=14, Hkv=2, D=64, bs=16, nb=32, scale=0.125, dtype=_lib.NS_DTYPE_F16, plan=None, plan_bytes=0,
              ws=16, ws_bytes=1 << 30, stream=None, aux=None, fork=None, join=None)
     a.update(over)
     return list(a.values())
@@ -71,6 +71,8 @@ def _attn_args(**over):
     (dict(aux=16), _lib.NS_ERR_INVALID_ARG),              # aux stream without its events
     (dict(aux=16, fork=16), _lib.NS_ERR_INVALID_ARG),
     (dict(aux=16, fork=16, join=16, stream=16), _lib.NS_ERR_INVALID_ARG),  # aux == stream
+    (dict(plan=16, plan_bytes=64), _lib.NS_ERR_INVALID_ARG),  # plan buffer smaller than the plan
+    (dict(plan=24, plan_bytes=1 << 20), _lib.NS_ERR_INVALID_ARG),  # misaligned plan
 ])
 def test_paged_attention_rejects_bad_arguments(over, code):
     lib = _lib.load()

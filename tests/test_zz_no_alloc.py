@@ -5,7 +5,7 @@ instead of a caller workspace, so its outputs must equal the workspace entry
 point's bit for bit.  Two calls in a row on the same scratch, the second with
 a smaller batch, check that a call leaves the scratch ready for the next (the
 split-K counters back at zero) whatever the shape; a mixed batch covers the
-prefill split state; a shape whose workspace exceeds the 64 MiB scratch is
+prefill split state; a shape whose workspace exceeds the 128 MiB scratch is
 refused with NS_ERR_WORKSPACE.
 """
 
@@ -38,7 +38,7 @@ def _args(case, out):
             None if qsl is None else qsl.data_ptr(), int(qsl is not None and qsl.dtype == torch.int64),
             lens, 1, qslh, 1,
             md.num_seqs, md.num_tokens, md.max_query_len, md.max_seq_len, int(md.is_decode_only),
-            Hq, Hkv, D, BS, NB, case.scale, _lib.DTYPE_CODES[q.dtype]]
+            Hq, Hkv, D, BS, NB, case.scale, _lib.DTYPE_CODES[q.dtype], None, 0]
 
 
 def _with_workspace(case):
@@ -84,12 +84,15 @@ def test_no_alloc_is_repeatable_and_refuses_oversized_shapes():
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     lib = _lib.load()
-    big = lib.ns_paged_attention_workspace_size(4096, 28, 4, 128, 16, 65536, 1, 4096, 1)
-    assert big > 64 << 20
+    # 256 sequences of up to 64K tokens, 16 query heads per kv head at head_dim
+    # 128: the plan fits the workspace's plan region, the decode split-K
+    # slots do not fit the scratch.
+    big = lib.ns_paged_attention_workspace_size(256, 64, 4, 128, 16, 65536, 1, 256, 1)
+    assert big > 128 << 20
     out = torch.empty(16, device=DEV)
     rc = lib.ns_paged_attention_noalloc(out.data_ptr(), out.data_ptr(), out.data_ptr(), out.data_ptr(),
                                         out.data_ptr(), 4096, 4096, 0, out.data_ptr(), 0, None, 0, None, 0,
-                                        None, 0, 4096, 4096, 1, 65536, 1, 28, 4, 128, 16, 1 << 20,
-                                        0.1, _lib.NS_DTYPE_BF16, torch.cuda.current_stream().cuda_stream,
+                                        None, 0, 256, 256, 1, 65536, 1, 64, 4, 128, 16, 1 << 20,
+                                        0.1, _lib.NS_DTYPE_BF16, None, 0, torch.cuda.current_stream().cuda_stream,
                                         None, None, None)
     assert rc == _lib.NS_ERR_WORKSPACE
