@@ -32,31 +32,19 @@ constexpr int kLdsSeqs = 2048;          // batches held in LDS
 constexpr int kEntryPasses = 4;         // items of 32 entries per thread pass: kThreads / 32 per pass
 constexpr int kItemsPerGroup = kThreads / 32 * kEntryPasses;
 
-__device__ __forceinline__ uint32_t wave_sum32(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-__device__ __forceinline__ uint64_t wave_sum64(uint64_t v) {
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
-__device__ __forceinline__ uint32_t wave_max32(uint32_t v) {
-  for (int off = 32; off > 0; off >>= 1) {
-    const uint32_t o = __shfl_xor(v, off);
-    v = o > v ? o : v;
-  }
-  return v;
-}
+// Wavefront reductions and scans of the device library (DPP lane moves, no
+// LDS round trips).
+extern "C" __device__ uint32_t __ockl_wfred_add_u32(uint32_t);
+extern "C" __device__ uint64_t __ockl_wfred_add_u64(uint64_t);
+extern "C" __device__ uint32_t __ockl_wfred_max_u32(uint32_t);
+extern "C" __device__ uint32_t __ockl_wfred_min_u32(uint32_t);
+extern "C" __device__ uint32_t __ockl_wfscan_add_u32(uint32_t, bool inclusive);
 
 // Exclusive prefix sum of v over the workgroup in thread order; `total` gets
 // the workgroup's sum.  `red` holds one word per wave.
 __device__ uint32_t block_exclusive_scan(uint32_t v, uint32_t& total, uint32_t* red) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  uint32_t x = v;
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint32_t y = __shfl_up(x, off);
-    if (lane >= off) x += y;
-  }
+  const uint32_t x = __ockl_wfscan_add_u32(v, true);
   if (lane == 63) red[w] = x;
   __syncthreads();
   uint32_t before = 0, all = 0;
@@ -79,6 +67,8 @@ struct alignas(16) PlanShared {
   uint64_t red64[kWaves];
   uint32_t red[kWaves], red2[kWaves];
   uint32_t fits[kWaves];
+  uint32_t cnt[kThreads];          // item counts of the candidate tokens per item
+  int32_t item_r[kItemsPerGroup];  // listed sequence of each of this workgroup's items
   int32_t len[kLdsSeqs], order[kLdsSeqs], qtok[kLdsSeqs];
   int32_t first[kLdsSeqs + 1];
 };
@@ -118,9 +108,9 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
       max_len = static_cast<uint32_t>(L) > max_len ? static_cast<uint32_t>(L) : max_len;
     }
   }
-  work = wave_sum64(work);
-  active = wave_sum32(active);
-  max_len = wave_max32(max_len);
+  work = __ockl_wfred_add_u64(work);
+  active = __ockl_wfred_add_u32(active);
+  max_len = __ockl_wfred_max_u32(max_len);
   if (lane == 0) {
     sh.red64[w] = work;
     sh.red[w] = active;
@@ -158,6 +148,26 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
     cb = clamp((pair_work + 16 * room - 1) / (16 * room));  // Hkv * (work / T + active) <= target
   }
   // Smallest fitting point of [ca, cb], or cb when none fits (cb is hi then).
+  // When candidates x sequences are few, every point below cb is counted in
+  // one pass (one (point, sequence) pair per thread and round, summed with
+  // LDS atomics); otherwise the waves narrow the range kWaves points a pass.
+  if (ca < cb && cb - ca <= kThreads && (cb - ca) * S <= 16 * kThreads) {
+    const int C = static_cast<int>(cb - ca);
+    for (int c = tid; c < C; c += kThreads) sh.cnt[c] = 0;
+    if (tid == 0) sh.fits[0] = static_cast<uint32_t>(C);
+    __syncthreads();
+    for (int u = tid; u < C * S; u += kThreads) {
+      const int c = u / S, sq = u - c * S;
+      const int32_t L = lens[sq];
+      if (L >= 0) atomicAdd(&sh.cnt[c], items_of(static_cast<uint32_t>(L), static_cast<uint32_t>((ca + c) * 16)));
+    }
+    __syncthreads();
+    for (int c = tid; c < C; c += kThreads)
+      if (static_cast<int64_t>(sh.cnt[c]) * Hkv <= target) atomicMin(&sh.fits[0], static_cast<uint32_t>(c));
+    __syncthreads();
+    ca += sh.fits[0];  // ca + C == cb when no point below cb fits
+    cb = ca;
+  }
   while (ca < cb) {
     const int64_t step = (cb - ca + kWaves - 1) / kWaves;
     const int64_t pt = ca + static_cast<int64_t>(w) * step;
@@ -168,7 +178,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
         const int32_t L = lens[s];
         if (L >= 0) n += items_of(static_cast<uint32_t>(L), T);
       }
-      n = wave_sum32(n);
+      n = __ockl_wfred_add_u32(n);
     }
     if (lane == 0) sh.fits[w] = pt < cb && static_cast<int64_t>(n) * Hkv <= target;
     __syncthreads();
@@ -190,9 +200,28 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
   }
   const uint32_t T = static_cast<uint32_t>(ca * 16);
 
-  // 3. List order: by decreasing length (ties by index) for batches held in
-  // LDS, else batch order; sequences that are not decode rows drop out.
-  if (in_lds) {
+  // 3. List order.  When every item runs at once (at most `cus` items) the
+  // order does not matter and the batch's own order is kept; otherwise
+  // decreasing length (ties by index) for batches held in LDS, so the longest
+  // pairs start first, else batch order.  Sequences that are not decode rows
+  // drop out.
+  uint32_t total = 0;
+  for (int s = tid; s < S; s += kThreads) {
+    const int32_t L = lens[s];
+    if (L >= 0) total += items_of(static_cast<uint32_t>(L), T);
+  }
+  total = __ockl_wfred_add_u32(total);
+  if (lane == 0) sh.red[w] = total;
+  __syncthreads();
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) total += sh.red[k];
+  __syncthreads();  // red is reused below
+  const bool one_round = static_cast<int64_t>(total) * Hkv <= a.cus;
+  const bool identity = one_round && static_cast<int>(active) == S;  // every sequence listed in place
+  if (identity) {
+    // order[r] = r: nothing to write.
+  } else if (in_lds && !one_round) {
     for (int s = tid; s < S; s += kThreads) {
       const int32_t L = lens[s];
       if (L < 0) continue;
@@ -221,12 +250,13 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
     }
   }
   __syncthreads();
+  auto listed = [&](int r) { return identity ? r : order[r]; };
 
   // 4. First item of each listed sequence: prefix sums of Hkv * n_s.
   uint32_t base = 0;
   for (int r0 = 0; r0 < static_cast<int>(active); r0 += kThreads) {
     const int r = r0 + tid;
-    const uint32_t n = r < static_cast<int>(active) ? items_of(lens[order[r]], T) * Hkv : 0u;
+    const uint32_t n = r < static_cast<int>(active) ? items_of(lens[listed(r)], T) * Hkv : 0u;
     uint32_t tot;
     const uint32_t f = base + block_exclusive_scan(n, tot, sh.red);
     if (r < static_cast<int>(active)) firstr[r] = static_cast<int32_t>(f);
@@ -247,6 +277,19 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
   const int64_t g0 = static_cast<int64_t>(blockIdx.x) * items_per_group;
   int64_t g1 = g0 + items_per_group;
   g1 = g1 < n_items ? g1 : n_items;
+  // A grid of small slices looks each item's listed sequence up in a table
+  // filled from the prefix sums; the single workgroup of a large batch
+  // searches them.
+  const bool table = items_per_group <= kItemsPerGroup;
+  if (table) {
+    for (int r = tid; r < static_cast<int>(active); r += kThreads) {
+      int64_t f0 = firstr[r], f1 = firstr[r + 1];
+      f0 = f0 > g0 ? f0 : g0;
+      f1 = f1 < g1 ? f1 : g1;
+      for (int64_t i = f0; i < f1; ++i) sh.item_r[i - g0] = r;
+    }
+    __syncthreads();
+  }
   for (int64_t i0 = g0; i0 < g1; i0 += kThreads / 32 * kEntryPasses) {
     uint32_t hw[kEntryPasses];
     int64_t id[kEntryPasses];
@@ -258,13 +301,18 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
       hw[ps] = 0;
       id[ps] = 0;
       if (idx >= g1) continue;
-      int lo_r = 0, hi_r = static_cast<int>(active) - 1;
-      while (lo_r < hi_r) {
-        const int mid = (lo_r + hi_r + 1) >> 1;
-        if (firstr[mid] <= idx) lo_r = mid;
-        else hi_r = mid - 1;
+      int lo_r = 0;
+      if (table) {
+        lo_r = sh.item_r[idx - g0];
+      } else {
+        int hi_r = static_cast<int>(active) - 1;
+        while (lo_r < hi_r) {
+          const int mid = (lo_r + hi_r + 1) >> 1;
+          if (firstr[mid] <= idx) lo_r = mid;
+          else hi_r = mid - 1;
+        }
       }
-      const int s = order[lo_r];
+      const int s = listed(lo_r);
       const uint32_t L = static_cast<uint32_t>(lens[s]);
       const uint32_t n = items_of(L, T);
       const uint32_t rel = static_cast<uint32_t>(idx - firstr[lo_r]);

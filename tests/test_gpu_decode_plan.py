@@ -10,7 +10,9 @@ against properties that do not restate how it is computed:
   * item sizes never exceed the plan's tokens per item, which is a multiple of
     16 no smaller than the minimum, and the item count stays within the
     buffer's capacity and the round target (or one item per pair);
-  * pairs are listed longest sequence first.
+  * a plan of more items than the device has CUs lists its pairs longest
+    sequence first (the items run in several rounds); a plan that runs in one
+    round keeps the batch's order.
 """
 
 from __future__ import annotations
@@ -99,10 +101,13 @@ def _check(seq_lens, query_lens, hkv=2, d=64, bs=16, index_dtype=torch.int64):
                         t = t0 + w * per_wave + 16 * (st * nt + j)
                         want = tables[s][t // bs] if t < end else 0
                         assert blk[(w * steps + st) * nt + j] == want, (s, t0, w, st, j)
-    # Longest sequence first, in item order.
+    # Longest sequence first when the items run in rounds; batch order otherwise.
     order = [int(items[i][0]) for i in range(n) if items[i][7] == 0 and items[i][6] == 0]
-    lens = [seq_lens[s] for s in order]
-    assert lens == sorted(lens, reverse=True)
+    if n > torch.cuda.get_device_properties(0).multi_processor_count:
+        lens = [seq_lens[s] for s in order]
+        assert lens == sorted(lens, reverse=True)
+    else:
+        assert order == sorted(order)
     return T, n
 
 
