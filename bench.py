@@ -571,6 +571,57 @@ def _time_steps(torch, steps, news, K, warmup, stream):
     }
 
 
+def _time_attn_variant(torch, steps, K, stream, per_step_plan=True, host_lists=True):
+    """Microseconds per attention call of K graph-replayed serving steps, for
+    the variants the line reports beside its main figure: the step's metadata
+    without any host-side lengths (host_lists=False: the engine's graph
+    replays, which never pass host copies), and every call building its own
+    decode plan (per_step_plan=False: a caller that does not share one plan
+    across the layers of a step)."""
+    import dataclasses
+
+    from nanoserve_amd import paged_attention_hip
+    from nanoserve_amd.attention import prepare_decode_plan
+
+    mds = {}
+    for st in steps:
+        md = st[0].md
+        if not host_lists:
+            md = dataclasses.replace(md, seq_lens_cpu=None, query_start_loc_cpu=None, query_lens_cpu=None)
+        md = dataclasses.replace(md, decode_plan=None)
+        mds[id(st[0].md)] = md
+    calls = [(c, mds[id(st[0].md)]) for st in steps for c in st]
+    R, L = len(steps), len(steps[0])
+
+    def run(n):
+        for j in range(n):
+            for i in range(j * L, (j + 1) * L):
+                c, md = calls[i]
+                if per_step_plan and i == j * L:
+                    prepare_decode_plan(md, c.k_cache)
+                paged_attention_hip(c.query, c.k_cache, c.v_cache, md, c.scale)
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        run(R)
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run(R)
+    reps = max(1, -(-K // R))
+    with torch.cuda.stream(stream):
+        g.replay()
+        stream.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(reps):
+            g.replay()
+        end.record(stream)
+    end.synchronize()
+    del g
+    return start.elapsed_time(end) * 1e3 / (reps * R * L)
+
+
 def main(argv=None):
     args = parse_args(argv)
     if args.gpus != 1:
@@ -610,6 +661,9 @@ def main(argv=None):
     dtype = calls[0].query.dtype
     dname = {torch.float16: "fp16", torch.bfloat16: "bf16"}[dtype]
     res = _time_steps(torch, steps, new_tokens(calls), K, args.warmup, stream)
+
+    no_host_us = _time_attn_variant(torch, steps, K, stream, per_step_plan=True, host_lists=False)
+    per_call_plan_us = _time_attn_variant(torch, steps, K, stream, per_step_plan=False, host_lists=False)
 
     eager_us = None
     if args.eager:
@@ -669,6 +723,12 @@ def main(argv=None):
             "frac": round(gbs / HBM_PEAK_GBS, 4),
             "traffic": traffic,
         },
+        "no_host_plan_us": round(no_host_us, 3),
+        "per_call_plan_us": round(per_call_plan_us, 3),
+        "plan_note": "the decode plan is built on the device from seq_lens in every variant: us_per_call and "
+                     "no_host_plan_us build it once per step (no_host_plan_us with the metadata's host-side "
+                     "lengths removed, as the engine's graph replays run); per_call_plan_us builds it inside "
+                     "every attention call",
         "reshape_and_cache_us": round(res["write_us"], 3),
         "rope_reshape_and_cache": {
             "us_per_call": round(res["rope_us"], 3),
