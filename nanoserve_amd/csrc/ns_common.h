@@ -107,6 +107,26 @@ __device__ __forceinline__ float group4_sum_swap(float v) {
   return x + y;
 }
 
+// Transposing LDS read (ds_read_b64_tr_b16) written as asm.  The builtin
+// carries no memory operand, so the compiler's wait-count pass assumes it may
+// read the destination of any LDS-DMA load in flight and puts an
+// s_waitcnt vmcnt(0) in front of it, which drains every prefetch of a
+// global_load_lds ring.  The asm result is not waited for: the caller issues
+// lds_wait_all() and then passes each result through lds_ready().
+__device__ __forceinline__ u32x2 ds_read_tr16_b64(const void* lds) {
+  u32x2 r;
+  const uint32_t a =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds)));
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Orders every later use of x after the preceding lds_wait_all().
+template <class V>
+__device__ __forceinline__ void lds_ready(V& x) {
+  asm volatile("" : "+v"(x));
+}
+
 // LDS ordering between lanes of one wave: LDS instructions of a wave execute
 // in order, so a compiler-level fence is enough to make one lane's ds_write
 // visible to another lane's later ds_read.

@@ -68,9 +68,13 @@ struct AttnParams {
   int pf_part_bytes;
   unsigned* pf_counters;
   int plan_n;             // prefill: sequences listed (0: no plan)
-  // Prefill schedule from host-side lengths and query offsets: two entries per
-  // listed sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
-  // slot_base | pair_base << 16, then its query length.
+};
+
+// The prefill kernel's arguments add its host-built schedule: two entries per
+// listed sequence y, s | (nsplit - 1) << 16 | split_macro << 22 and
+// slot_base | pair_base << 16, then its query length.  The decode kernel takes
+// the 200-byte base alone, so its launches do not carry the 3 KB schedule.
+struct PrefillParams : AttnParams {
   uint32_t plan[kPlanMax];
 };
 
@@ -550,6 +554,11 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
   WaveBlocks<W, CH> ib;
   load_item<W, CH>(p, idx, r0, r1, ib);
   const uint32_t n_hdr = p.plan_hdr->n_items;
+  // Both scalar loads are in flight before either is waited for (the
+  // compiler would otherwise sink the item's load below the count check:
+  // two round trips before the first K/V load instead of one).
+  asm volatile("" ::"s"(n_hdr), "s"(r0), "s"(r1), "s"(ib.id[0]), "s"(ib.id[1]), "s"(ib.id[2]), "s"(ib.id[3]),
+               "s"(ib.id[4]), "s"(ib.id[5]), "s"(ib.id[6]), "s"(ib.id[7]));
   const uint32_t n_items = n_hdr < p.item_cap ? n_hdr : static_cast<uint32_t>(p.item_cap);
   while (idx < n_items) {
     decode_item<DT, D, W, CH, BTI, BIG>(p, idx, r0, r1, ib, smem, later_lds, s_merger);
@@ -630,7 +639,7 @@ __device__ __forceinline__ void stage_barrier() {
 constexpr int kPrefillThreads = 512;
 
 template <class DT, int D, int CT, class BTI>
-__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(AttnParams p) {
+__global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillParams p) {
   using Cfg = PrefillCfg<D, CT>;
   static_assert(Cfg::THREADS == kPrefillThreads, "launch bounds match the workgroup");
   using T = typename DT::T;
@@ -1280,7 +1289,7 @@ hipError_t launch_decode_rows(AttnParams& p, const DecodePlanArgs* build, int gr
 // ordinary cross-stream dependencies.  Without one the launches run in order
 // on `stream`.
 template <class DT, int D>
-hipError_t launch_attention(AttnParams& p, AttnParams& pp, const DecodePlanArgs* build, int decode_grid,
+hipError_t launch_attention(AttnParams& p, PrefillParams& pp, const DecodePlanArgs* build, int decode_grid,
                             int pf_grid_x, bool launch_decode, int num_seqs, int max_query_len, hipStream_t stream,
                             const AuxStream* aux) {
   if (p.decode_only) return launch_decode_rows<DT, D>(p, build, decode_grid, stream);
@@ -1332,7 +1341,7 @@ int64_t host_index(const void* a, int is64, int64_t i) {
 // chunk); splits need partial slots, so the share doubles until the slots
 // fit.  Returns the sequences listed (0: no plan, the launch then uses the
 // full grid without splits) and the grid width.
-int build_prefill_plan(AttnParams& pp, const void* lens, int lens64, const void* qsl, int qsl64, int num_seqs,
+int build_prefill_plan(PrefillParams& pp, const void* lens, int lens64, const void* qsl, int qsl64, int num_seqs,
                        int cols_per_wg, int macro_keys, int& grid_x) {
   constexpr int kCUs = 256, kMinSplitMacro = 4, kMaxListed = kPlanMax / 3;
   struct Seq {
@@ -1646,10 +1655,10 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
                           host_index(qsl_host, query_start_loc_host_is_int64, i) == 1;
   }
   // Prefill plan (split-K over the CUs) from host offsets and lengths.
-  AttnParams pp;
+  PrefillParams pp;
   int pf_grid_x = 0;
   if (!is_decode_only) {
-    pp = p;
+    static_cast<AttnParams&>(pp) = p;
     pp.plan_n = 0;
     if (seq_lens_host && qsl_host) {
       const int mkeys = head_dim == 64 ? PrefillCfg<64, kPrefillTiles>::KG * PrefillCfg<64, kPrefillTiles>::KT
