@@ -120,6 +120,45 @@ __device__ __forceinline__ u32x2 ds_read_tr16_b64(const void* lds) {
   asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
   return r;
 }
+// global_load_lds as asm: each lane's `bytes` (4 or 16) at `src` land in
+// LDS at lds + bytes * lane.  The compiler does not see these loads, so its
+// wait-count pass neither waits for them (the caller does, with explicit
+// vmcnt) nor drains them before later LDS or DMA instructions; its own
+// waits for its own loads only ever count too few operations in flight,
+// which waits longer, never too little.
+// M0 is reserved, so listing it as clobbered draws a warning; the compiler
+// sets M0 itself right before any instruction of its own that reads it.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma_lds16(const void* src, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4(const void* src, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src), "s"(m) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// Plain LDS reads as asm, for data that arrived by global_load_lds: the
+// compiler's wait-count pass would otherwise wait for every LDS-DMA load in
+// flight before any LDS read it cannot prove disjoint from them.
+__device__ __forceinline__ u32x4 ds_read_b128(const void* lds) {
+  u32x4 r;
+  const uint32_t a =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds)));
+  asm volatile("ds_read_b128 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
+__device__ __forceinline__ uint32_t ds_read_b32(const void* lds) {
+  uint32_t r;
+  const uint32_t a =
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds)));
+  asm volatile("ds_read_b32 %0, %1" : "=v"(r) : "v"(a));
+  return r;
+}
 __device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 // Orders every later use of x after the preceding lds_wait_all().
 template <class V>

@@ -78,24 +78,77 @@ struct PrefillParams : AttnParams {
   uint32_t plan[kPlanMax];
 };
 
+typedef short short4_t __attribute__((ext_vector_type(4)));
+
+// Address-space views for global_load_lds (global source, LDS destination).
+typedef __attribute__((address_space(1))) void* gbl_void_ptr;
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// LDS swizzles of K and V tiles ([keys][D] rows of 16-byte units): unit c of
+// key k is stored at unit c ^ k_swz(k) (K) or c ^ v_swz(k) (V) of its row, so
+// the 16-byte K operand reads and the 8-byte transposing V reads of a wave
+// spread over all banks.  A DMA lane picks the global unit that belongs at
+// its LDS slot, so the swizzle costs nothing on the write side.
+__device__ __forceinline__ int k_swz(int key) { return key & 7; }
+__device__ __forceinline__ int v_swz(int key) { return (key & 3) << 1; }
+
 // --------------------------------------------------------------------------
 // Decode: one workgroup of W waves per plan item (a token range of one
 // (sequence, kv head) pair); the grid loops over the plan's items.
 // --------------------------------------------------------------------------
-template <int D, int W, int CH_>
+// A wave walks its tokens in chunks of 32 (two 16-token MFMA tiles).  Chunks
+// go from HBM into a ring of R slots in the wave's own LDS with
+// global_load_lds, so loads in flight hold no registers and every wait for
+// them is an explicit vmcnt the wave chooses; the query tile and the block
+// ids past the item's carried ones arrive the same way, ahead of the first
+// chunk.
+template <int D, int W, int R_>
 struct DecodeCfg {
   static constexpr int kThreads = W * 64;
-  static constexpr int CH = CH_;                // tokens per wave per step
-  static constexpr int NT = CH / 16;            // 16-token MFMA tiles per step
-  static constexpr int NC = D / 32;             // k-chunks of the QK^T contraction
-  static constexpr int NN = D / 16;             // 16-dim tiles of the output
-  static constexpr int VT_LD = CH + 4;          // padded row of the transposed V tile
-  static constexpr int LDS_V = W * D * VT_LD * 2;
-  static constexpr int RED_LD = D + 4;             // padded row of the cross-wave reduce
-  static constexpr int LDS_RED = (W * 16 * RED_LD + 2 * W * 16) * 4;
-  static constexpr int LDS = LDS_V > LDS_RED ? LDS_V : LDS_RED;
-  static_assert(NT % 2 == 0, "P^T operand pairs two 16-token tiles");
+  static constexpr int CHUNK = 32;               // tokens per chunk
+  static constexpr int NC = D / 32;              // k-chunks of the QK^T contraction
+  static constexpr int NN = D / 16;              // 16-dim tiles of the output
+  static constexpr int CPR = D / 8;              // 16-byte units per token row
+  static constexpr int TILE_B = CHUNK * D * 2;   // bytes of a chunk's K (or V)
+  static constexpr int DMA = TILE_B / 1024;      // global_load_lds per K (or V) of a chunk
+  static constexpr int PER_CHUNK = 2 * DMA;      // vector-memory operations per chunk
+  static constexpr int R = R_;                   // ring slots per wave
+  static constexpr int SLOT_B = 2 * TILE_B;
+  static constexpr int QD = 16 * D * 2 / 1024;   // global_load_lds of the 16-row query tile
+  static constexpr int Q_B = QD * 1024;
+  static constexpr int IDC_B = 64;               // the item's carried block ids (8 int32)
+  static constexpr int IDS_B = 512;              // later block-table entries: 64 low words, 64 high words
+  static constexpr int WAVE_B = R * SLOT_B + Q_B + IDC_B + IDS_B;
+  static constexpr int RED_LD = D + 4;           // padded row of a wave's block in the cross-wave reduce
+  static constexpr int LDS = W * WAVE_B;
+  static_assert((R - 1) * PER_CHUNK <= 63, "waits fit vmcnt");
+  static_assert(2 * R <= kItemBlocks / W, "the first R chunks' tiles are carried by the item");
 };
+
+// Wait until at most k chunks (k * PC vector-memory operations) of this wave
+// are in flight; k is wave-uniform and below R.
+template <int PC, int R>
+__device__ __forceinline__ void wait_chunks(int k) {
+  if constexpr (R > 3) {
+    if (k >= 3) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PC) : "memory");
+      return;
+    }
+  }
+  if constexpr (R > 2) {
+    if (k >= 2) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PC) : "memory");
+      return;
+    }
+  }
+  if constexpr (R > 1) {
+    if (k >= 1) {
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PC) : "memory");
+      return;
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
 
 // Split-K state crosses workgroups (and XCDs, whose L2s are not coherent
 // with each other) through device-scope accesses: stores with the SC1 cache
@@ -203,24 +256,17 @@ __device__ void merge_partials(const AttnParams& p, __amdgpu_buffer_rsrc_t pr, u
 
 // One plan item: context tokens [t0, t1) of (sequence s, kv head), read once
 // and used by all G query heads of the group.  The item's 16-token tiles are
-// dealt out evenly, each wave a contiguous run walked CH tokens per step with
-// the next step's K/V loads (and the step after's table entries) in flight.
-// A wave's share of an item's carried block ids: steps IS of NT tiles.
-template <int W, int CH>
+// dealt out evenly, each wave a contiguous run.  The item carries the block
+// ids of each wave's first eight tiles.
 struct WaveBlocks {
-  static constexpr int NT = CH / 16;
-  static constexpr int IS = kItemBlocks / (W * NT);
-  static constexpr int N = IS * NT;
-  static_assert(N == 8, "two 16-byte rows per wave");
-  int32_t id[N];
+  int32_t id[8];
 };
 
 // The item rows and this wave's carried block ids of plan item idx (uniform
 // per wave, so they come through the scalar cache, outside the vector-memory
 // order the K/V loads keep).
-template <int W, int CH>
 __device__ __forceinline__ void load_item(const AttnParams& p, uint32_t idx, u32x4& r0, u32x4& r1,
-                                          WaveBlocks<W, CH>& wb) {
+                                          WaveBlocks& wb) {
   const u32x4* rows = reinterpret_cast<const u32x4*>(p.items + idx);
   r0 = rows[0];
   r1 = rows[1];
@@ -234,17 +280,15 @@ __device__ __forceinline__ void load_item(const AttnParams& p, uint32_t idx, u32
   }
 }
 
-template <class DT, int D, int W, int CH, class BTI, bool BIG>
+template <class DT, int D, int W, int R, class BTI, bool BIG>
 __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u32x4 r0, u32x4 r1,
-                                            const WaveBlocks<W, CH>& ib, char* smem, int64_t* later_lds,
-                                            int& s_merger) {
-  using Cfg = DecodeCfg<D, W, CH>;
+                                            const WaveBlocks& ib, char* smem, int& s_merger) {
+  using Cfg = DecodeCfg<D, W, R>;
   using T = typename DT::T;
   using V8 = typename DT::vec8;
   constexpr int THREADS = Cfg::kThreads;
-  constexpr int NT = Cfg::NT, NC = Cfg::NC, NN = Cfg::NN, VT_LD = Cfg::VT_LD;
-  constexpr int IS = WaveBlocks<W, CH>::IS;
-  static_assert(W == kItemWaves, "items carry the block ids of kItemWaves waves");
+  constexpr int NC = Cfg::NC, NN = Cfg::NN, CPR = Cfg::CPR, DMA = Cfg::DMA, PC = Cfg::PER_CHUNK;
+  constexpr int TILE_B = Cfg::TILE_B, SLOT_B = Cfg::SLOT_B;
 
   const int s = static_cast<int>(r0[0]);
   const int64_t qtok = r0[1], t0 = r0[2], t1 = r0[3];
@@ -257,235 +301,401 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
       static_cast<int64_t>(first) + nsplit > p.item_cap)
     return;
 
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: keeps the chunk logic scalar
   const int64_t pair = static_cast<int64_t>(s) * Hkv + kvh;
 
-  const int bs_mask = (1 << p.bs_shift) - 1;
+  const int bs_shift = p.bs_shift;
+  const int64_t bs_mask = (int64_t{1} << bs_shift) - 1;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
   const int64_t tiles = (t1 - t0 + 15) >> 4;
   const int64_t per_wave = (tiles + W - 1) / W * 16;
   const int64_t wb = t0 + w * per_wave;
   const int64_t we = t1 < wb + per_wave ? t1 : wb + per_wave;  // wave w's tokens: [wb, we)
+  const int nch = wb < we ? static_cast<int>((we - wb + 31) >> 5) : 0;
+  const int wtiles = wb < we ? static_cast<int>((we - wb + 15) >> 4) : 0;
 
-  V8 qop[NC];
-  {
-    const int hq = c16 < G ? c16 : G - 1;  // in-row address for the padding columns
-    const T* qrow = reinterpret_cast<const T*>(p.query) +
-                    (qtok * p.num_heads + static_cast<int64_t>(kvh) * G + hq) * D;
-#pragma unroll
-    for (int c = 0; c < NC; ++c) qop[c] = load16<DT>(qrow + 32 * c + 8 * g);
-    if (c16 >= G)
-#pragma unroll
-      for (int c = 0; c < NC; ++c) qop[c] = zero8<DT>();
-  }
   T* out_row = reinterpret_cast<T*>(p.out) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
+  const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between token rows
+  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D;
+  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D;
 
-  T* vt = reinterpret_cast<T*>(smem) + w * D * VT_LD;  // this wave's V^T tile [D][VT_LD]
+  // This wave's LDS: the chunk ring, the query tile, carried and later block ids.
+  char* ring = smem + w * Cfg::WAVE_B;
+  char* qlds = ring + R * SLOT_B;
+  int32_t* idc = reinterpret_cast<int32_t*>(qlds + Cfg::Q_B);
+  char* ids = qlds + Cfg::Q_B + Cfg::IDC_B;
+
   int bad = 0;
   float m_run = -INFINITY, l_run = 0.f;
   floatx4 acc[NN];
 #pragma unroll
   for (int n = 0; n < NN; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
-  const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;  // elements between slots
-  const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
-  const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D + 8 * g;
-  const T* zbase = reinterpret_cast<const T*>(p.zeros) + 8 * g;  // a never-written zero page
 
-  // Issue the K/V loads of the step starting at token tb.  Lanes past the
-  // wave's range or with an invalid block id read the zero page, so their V
-  // contributes nothing (their scores are masked) and nothing here or later
-  // waits on the data to fix it up.
-  auto issue_step = [&](int64_t tb, const int64_t (&bk)[NT], V8 (&kx)[NT][NC], V8 (&vx)[NT][NC]) {
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      const int64_t t = tb + 16 * j + c16;
-      bool valid = t < we;
-      if (valid && (bk[j] < 0 || bk[j] >= p.num_blocks)) {
-        bad = 1;
-        valid = false;
-      }
-      const int64_t off = ((bk[j] << p.bs_shift) + (t & bs_mask)) * slot_stride;
-      const T* kp = valid ? kbase + off : zbase;
-      const T* vp = valid ? vbase + off : zbase;
-#pragma unroll
-      for (int c = 0; c < NC; ++c) {
-        kx[j][c] = load16<DT>(kp + 32 * c);
-        vx[j][c] = load16<DT>(vp + 32 * c);
-      }
-    }
-  };
-
-  // Where the block ids of every step come from.  BIG (block size >= 16: a
-  // tile lies in one block): the item carries those of the wave's first IS
-  // steps, and the ids of its later tiles come in one vector load (lane l:
-  // tile IS * NT + l) issued before any K/V load and staged in LDS, so the
-  // step loop reads them with LDS loads.  Vector-memory loads return in
-  // order, and this way no K/V load waits for another step's data.  (The
-  // plan caps an item at 4096 tokens, which keeps a wave within IS * NT + 64
-  // tiles.)  Smaller blocks: per-lane block-table entries per step, clamped
-  // into the wave's range.
-  const int64_t nsteps = wb < we ? (we - wb + CH - 1) / CH : 0;
-  // Loads in the BIG kernel are unconditional (clamped addresses, or the
-  // zero page), so the compiler can count them exactly: a wait for one step's
-  // data never turns into a wait for everything in flight.
-  int64_t later_ids = 0;
-  if constexpr (BIG) {
-    int64_t t = wb + 16 * (IS * NT + lane);
-    t = t < we ? t : we - 1;
-    t = t > 0 ? t : 0;
-    later_ids = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
-  }
-  int64_t* my_later = later_lds + w * 64;
-  auto step_blocks = [&](int64_t st, int64_t (&bk)[NT]) {
-    if constexpr (BIG) {
-      if (st < IS) {
-#pragma unroll
-        for (int q = 0; q < IS; ++q)
-          if (q == st)
-#pragma unroll
-            for (int j = 0; j < NT; ++j) bk[j] = ib.id[q * NT + j];
-      } else {
-        const int64_t* src = my_later + (st - IS) * NT;
-#pragma unroll
-        for (int j = 0; j < NT; ++j) bk[j] = src[j];
-      }
+  // Block id of the wave's tile `tile` for a chunk past the first R (BIG):
+  // the carried ones from idc, the later ones from the table entries the
+  // wave loaded into `ids`.  Uniform, so the DMA addresses stay scalar.
+  const int64_t e_first = (wb + 128) >> bs_shift;  // table entry of tile 8
+  auto tile_block = [&](int tile) -> int64_t {
+    uint32_t lo, hi = 0;
+    if (tile < 8) {
+      lo = ds_read_b32(idc + tile);
     } else {
+      const int64_t e = ((wb + 16 * static_cast<int64_t>(tile)) >> bs_shift) - e_first;
+      lo = ds_read_b32(ids + 4 * e);
+      if constexpr (sizeof(BTI) == 8) hi = ds_read_b32(ids + 256 + 4 * e);
+    }
+    lds_wait_all();
+    lds_ready(lo);
+    lds_ready(hi);
+    if constexpr (sizeof(BTI) == 4) hi = static_cast<uint32_t>(static_cast<int32_t>(lo) >> 31);
+    lo = __builtin_amdgcn_readfirstlane(lo);
+    hi = __builtin_amdgcn_readfirstlane(hi);
+    return static_cast<int64_t>(static_cast<uint64_t>(hi) << 32 | lo);
+  };
+
+  // Start chunk ci's K and V loads into ring slot `slot`.  LDS unit u * 64 +
+  // lane of a tile holds token k = unit / CPR of the chunk, unit position
+  // unit % CPR; a token past the wave's range loads token we - 1 again (the
+  // same addresses as a lane that needs it, so no extra traffic) and is
+  // masked when read.  BIG: one load covers tokens of one 16-token tile,
+  // whose block id (blk_a for the first tile, blk_b for the second) is
+  // uniform.  Otherwise every lane reads its token's table entry.
+  auto issue_chunk = [&](int ci, int slot, int64_t blk_a, int64_t blk_b) {
+    const int64_t tb = wb + 32 * static_cast<int64_t>(ci);
+    char* kd = ring + slot * SLOT_B;
+    char* vd = kd + TILE_B;
 #pragma unroll
-      for (int j = 0; j < NT; ++j) {
-        int64_t t = wb + st * CH + 16 * j + c16;
-        t = t < we ? t : we - 1;
-        t = t > 0 ? t : 0;
-        bk[j] = ld_idx<BTI>(p.bt, bt_row + (t >> p.bs_shift));
+    for (int u = 0; u < DMA; ++u) {
+      const int unit = u * 64 + lane;
+      const int k = unit / CPR, pc = unit % CPR;
+      int64_t t = tb + k;
+      t = t < we ? t : we - 1;
+      int64_t blk;
+      if constexpr (BIG) {
+        blk = (u * 64) / CPR < 16 ? blk_a : blk_b;
+      } else {
+        blk = ld_idx<BTI>(p.bt, bt_row + (t >> bs_shift));
       }
+      if (blk < 0 || blk >= p.num_blocks) {
+        bad = 1;
+        blk = 0;
+      }
+      const int64_t row = ((blk << bs_shift) + (t & bs_mask)) * slot_stride;
+      dma_lds16(kbase + row + ((pc ^ k_swz(k)) << 3), kd + u * 1024);
+      dma_lds16(vbase + row + ((pc ^ v_swz(k)) << 3), vd + u * 1024);
     }
   };
 
-  // Software pipeline over the wave's steps: step st + 1's K/V loads are in
-  // flight while step st computes.
-  V8 kr[NT][NC], vr[NT][NC];
-  if (BIG || nsteps > 0) {
-    int64_t bk[NT];
-    step_blocks(0, bk);
-    issue_step(wb, bk, kr, vr);
-  }
-  if constexpr (BIG) {
-    my_later[lane] = later_ids;  // waits for the id load only: it went out before the K/V loads
-    wave_lds_sync();
-  }
-  for (int64_t st = 0; st < nsteps; ++st) {
-    const int64_t tb = wb + st * CH;
-    const bool has_next = st + 1 < nsteps;
-    V8 kn[NT][NC], vn[NT][NC];
-    if (BIG || has_next) {
-      // (BIG: past the wave's last step every lane reads the zero page.)
-      int64_t bk[NT];
-      step_blocks(has_next ? st + 1 : st, bk);
-      issue_step(tb + CH, bk, kn, vn);
+  V8 qop[NC];
+  // One chunk from ring slot `slot`: S^T = K Q^T (sacc[h][r]: token 16h + 4g
+  // + r of the chunk, head c16), the online softmax, O^T += V^T P^T.
+  auto compute_chunk = [&](int ci, int slot) {
+    const int64_t tb = wb + 32 * static_cast<int64_t>(ci);
+    const char* kt = ring + slot * SLOT_B;
+    const char* vt = kt + TILE_B;
+    // Every LDS read of the chunk goes out before one wait: K rows (key
+    // 16h + c16, dims 32c + 8g ..) and the transposing V^T reads
+    // (ds_read_b64_tr_b16 gives lane c16 of group g V^T row 16n + c16 at keys
+    // 16h + 4g + 0..3 when it points at dims 16n + 4 (c16 & 3) .. +3 of key
+    // 16h + 4g + (c16 >> 2)).
+    u32x4 kraw[2][NC];
+    u32x2 hop[NN][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int key = 16 * h + c16;
+#pragma unroll
+      for (int c = 0; c < NC; ++c) kraw[h][c] = ds_read_b128(kt + key * D * 2 + (((4 * c + g) ^ k_swz(key)) << 4));
     }
-    // Scheduling boundary: the next step's loads are issued before anything
-    // below uses (and so waits for) this step's K/V registers.  The empty asm
-    // takes them as in/out operands, so nothing that reads them can be
-    // hoisted above it, and its memory clobber keeps the loads above it.
-    asm volatile("" ::: "memory");
+    const int d0 = 4 * (c16 & 3);
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int n = 0; n < NN; ++n)
 #pragma unroll
-      for (int c = 0; c < NC; ++c) asm volatile("" : "+v"(kr[j][c]), "+v"(vr[j][c]));
-    // Stage V transposed (vt[dim][token]) for the PV operand.
+      for (int h = 0; h < 2; ++h) {
+        const int key = 16 * h + 4 * g + (c16 >> 2);
+        const int d = 16 * n + d0;
+        hop[n][h] = ds_read_tr16_b64(vt + key * D * 2 + (((d >> 3) ^ v_swz(key)) << 4) + ((d & 7) << 1));
+      }
+    lds_wait_all();
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
-      for (int c = 0; c < NC; ++c)
+      for (int c = 0; c < NC; ++c) lds_ready(kraw[h][c]);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) vt[(32 * c + 8 * g + e) * VT_LD + 16 * j + c16] = vr[j][c][e];
-
-    // S^T = K Q^T: sacc[j][r] = score of token tb + 16j + 4g + r, head c16.
-    floatx4 sacc[NT];
-#pragma unroll
-    for (int j = 0; j < NT; ++j) {
-      sacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int c = 0; c < NC; ++c) sacc[j] = mfma16x16x32(DT{}, kr[j][c], qop[c], sacc[j]);
+    for (int n = 0; n < NN; ++n) {
+      lds_ready(hop[n][0]);
+      lds_ready(hop[n][1]);
     }
-    float sv[NT][4];
+    floatx4 sacc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sacc[h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < NC; ++c) sacc[h] = mfma16x16x32(DT{}, __builtin_bit_cast(V8, kraw[h][c]), qop[c], sacc[h]);
+    }
+    float sv[2][4];
     float mloc = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t t = tb + 16 * j + 4 * g + r;
-        const float x = t < we ? sacc[j][r] * p.scale_log2 : -INFINITY;
-        sv[j][r] = x;
+        const float x = tb + 16 * h + 4 * g + r < we ? sacc[h][r] * p.scale_log2 : -INFINITY;
+        sv[h][r] = x;
         mloc = fmaxf(mloc, x);
       }
-    mloc = group4_max(mloc);
+    mloc = group4_max_swap(mloc);
     const float m_new = fmaxf(m_run, mloc);
     const bool none = m_new == -INFINITY;
     const float alpha = none ? 1.f : fast_exp2(m_run - m_new);
     float psum = 0.f;
 #pragma unroll
-    for (int j = 0; j < NT; ++j)
+    for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const float pr = none ? 0.f : fast_exp2(sv[j][r] - m_new);
-        sv[j][r] = pr;
+        const float pr = none ? 0.f : fast_exp2(sv[h][r] - m_new);
+        sv[h][r] = pr;
         psum += pr;
       }
     l_run = l_run * alpha + psum;
 #pragma unroll
     for (int n = 0; n < NN; ++n) acc[n] *= alpha;
     m_run = m_new;
-
-    wave_lds_sync();
-    // O^T += V^T P^T over 32-token pairs: k-slot e of group g is token 4g+e of
-    // the even tile (e < 4) or of the odd tile (e >= 4).
+    // P^T operand: k-slot e of group g is token 4g + e of tile 0 (e < 4) or
+    // of tile 1 (e >= 4), matching the V^T reads above.
+    V8 pt;
 #pragma unroll
-    for (int pb = 0; pb < NT / 2; ++pb) {
-      V8 pt;
+    for (int e = 0; e < 4; ++e) {
+      pt[e] = static_cast<T>(sv[0][e]);
+      pt[4 + e] = static_cast<T>(sv[1][e]);
+    }
+    // Tokens past the wave's range hold a copy of token we - 1: their V
+    // elements are zeroed (their P is zero, but V may hold inf or NaN).
+    const bool vfull = tb + 32 <= we;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pt[e] = static_cast<T>(sv[2 * pb][e]);
-        pt[4 + e] = static_cast<T>(sv[2 * pb + 1][e]);
+    for (int n = 0; n < NN; ++n) {
+      V8 va = __builtin_bit_cast(V8, u32x4{hop[n][0][0], hop[n][0][1], hop[n][1][0], hop[n][1][1]});
+      if (!vfull) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int key = 16 * (e >> 2) + 4 * g + (e & 3);
+          va[e] = tb + key < we ? va[e] : static_cast<T>(0.f);
+        }
       }
+      acc[n] = mfma16x16x32(DT{}, va, pt, acc[n]);
+    }
+  };
+
+  // All nch (<= R) chunks of the wave from ring slots 0 .. nch-1 at once.
+  auto compute_all = [&](int n_ch) {
+    floatx4 sacc[R][2];
 #pragma unroll
-      for (int n = 0; n < NN; ++n) {
-        const T* r0p = vt + (16 * n + c16) * VT_LD + 32 * pb + 4 * g;
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(r0p);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(r0p + 16);
-        const V8 va = __builtin_bit_cast(V8, u32x4{lo[0], lo[1], hi[0], hi[1]});
-        acc[n] = mfma16x16x32(DT{}, va, pt, acc[n]);
+    for (int ci = 0; ci < R; ++ci) {
+      if (ci < n_ch) {
+        const char* kt = ring + ci * SLOT_B;
+        u32x4 kraw[2][NC];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int key = 16 * h + c16;
+#pragma unroll
+          for (int c = 0; c < NC; ++c)
+            kraw[h][c] = ds_read_b128(kt + key * D * 2 + (((4 * c + g) ^ k_swz(key)) << 4));
+        }
+        lds_wait_all();
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          sacc[ci][h] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int c = 0; c < NC; ++c) {
+            lds_ready(kraw[h][c]);
+            sacc[ci][h] = mfma16x16x32(DT{}, __builtin_bit_cast(V8, kraw[h][c]), qop[c], sacc[ci][h]);
+          }
+        }
       }
     }
-    wave_lds_sync();
-    if (has_next) {
+    float mloc = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < NT; ++j)
+    for (int ci = 0; ci < R; ++ci)
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t t = wb + 32 * ci + 16 * h + 4 * g + r;
+          const float x = ci < n_ch && t < we ? sacc[ci][h][r] * p.scale_log2 : -INFINITY;
+          sacc[ci][h][r] = x;
+          mloc = fmaxf(mloc, x);
+        }
+    const float m = group4_max_swap(mloc);
+    const bool none = m == -INFINITY;
+    float psum = 0.f;
+    const int d0 = 4 * (c16 & 3);
+#pragma unroll
+    for (int ci = 0; ci < R; ++ci) {
+      if (ci < n_ch) {
+        V8 pt;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float pr = none ? 0.f : fast_exp2(sacc[ci][h][r] - m);
+            psum += pr;
+            pt[4 * h + r] = static_cast<T>(pr);
+          }
+        const char* vt = ring + ci * SLOT_B + TILE_B;
+        u32x2 hop[NN][2];
+#pragma unroll
+        for (int n = 0; n < NN; ++n)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) {
+            const int key = 16 * h + 4 * g + (c16 >> 2);
+            const int d = 16 * n + d0;
+            hop[n][h] = ds_read_tr16_b64(vt + key * D * 2 + (((d >> 3) ^ v_swz(key)) << 4) + ((d & 7) << 1));
+          }
+        lds_wait_all();
+        const int64_t tb = wb + 32 * ci;
+        const bool vfull = tb + 32 <= we;
+#pragma unroll
+        for (int n = 0; n < NN; ++n) {
+          lds_ready(hop[n][0]);
+          lds_ready(hop[n][1]);
+          V8 va = __builtin_bit_cast(V8, u32x4{hop[n][0][0], hop[n][0][1], hop[n][1][0], hop[n][1][1]});
+          if (!vfull) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              const int key = 16 * (e >> 2) + 4 * g + (e & 3);
+              va[e] = tb + key < we ? va[e] : static_cast<T>(0.f);
+            }
+          }
+          acc[n] = mfma16x16x32(DT{}, va, pt, acc[n]);
+        }
+      }
+    }
+    m_run = none ? -INFINITY : m;
+    l_run = psum;
+  };
+
+  if (nch > 0) {
+    // The query tile (rows: the group's heads; rows past G repeat the last
+    // head and are zeroed when read), then, for waves with more than eight
+    // tiles, the table entries from tile 8 on: both land before chunk 0.
+    if constexpr (BIG) {
+      // Carried ids to LDS for chunks past the first R, before any DMA is
+      // in flight (one lane, two 16-byte stores).
+      if (nch > R && lane == 0) {
+        *reinterpret_cast<u32x4*>(idc) = u32x4{static_cast<uint32_t>(ib.id[0]), static_cast<uint32_t>(ib.id[1]),
+                                               static_cast<uint32_t>(ib.id[2]), static_cast<uint32_t>(ib.id[3])};
+        *reinterpret_cast<u32x4*>(idc + 4) = u32x4{static_cast<uint32_t>(ib.id[4]), static_cast<uint32_t>(ib.id[5]),
+                                                   static_cast<uint32_t>(ib.id[6]), static_cast<uint32_t>(ib.id[7])};
+      }
+      wave_lds_sync();
+    }
+    {
+      const T* qg = reinterpret_cast<const T*>(p.query) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
+#pragma unroll
+      for (int u = 0; u < Cfg::QD; ++u) {
+        const int unit = u * 64 + lane;
+        int row = unit / CPR;
+        row = row < G ? row : G - 1;
+        dma_lds16(qg + row * D + (unit % CPR) * 8, qlds + u * 1024);
+      }
+    }
+    if constexpr (BIG) {
+      {
+        // Lane l: entry e_first + l (at most the wave's last), low words at
+        // ids[l], high words (int64 tables) at ids[64 + l].  Issued by every
+        // wave (a wave with eight tiles or fewer reads its last entry), so no
+        // branch separates these loads from the chunks'.
+        const int64_t e_last = (we - 1) >> bs_shift;
+        int64_t e = e_first + lane;
+        e = e <= e_last ? e : e_last;
+        const char* src = reinterpret_cast<const char*>(reinterpret_cast<const BTI*>(p.bt) + bt_row + e);
+        dma_lds4(src, ids);
+        if constexpr (sizeof(BTI) == 8) dma_lds4(src + 4, ids + 256);
+      }
+    }
+    // Chunks 0 .. R-1 (their tiles' block ids come with the item).
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (r < nch) {
+        if constexpr (BIG) {
+          const int64_t a = ib.id[2 * r];
+          issue_chunk(r, r, a, 2 * r + 1 < wtiles ? static_cast<int64_t>(ib.id[2 * r + 1]) : a);
+        } else {
+          issue_chunk(r, r, 0, 0);
+        }
+      }
+    if (nch <= R) {
+      // Every chunk of the wave is in flight: they land at about the same
+      // time, so they are processed together (one maximum, one pass of
+      // exponentials) instead of one dependent online-softmax step each.
+      wait_chunks<PC, R>(0);
+      u32x4 qraw[NC];
+#pragma unroll
+      for (int c = 0; c < NC; ++c) qraw[c] = ds_read_b128(qlds + c16 * D * 2 + (4 * c + g) * 16);
+      lds_wait_all();
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        lds_ready(qraw[c]);
+        qop[c] = c16 < G ? __builtin_bit_cast(V8, qraw[c]) : zero8<DT>();
+      }
+      compute_all(nch);
+    } else
+    for (int ci = 0; ci < nch; ++ci) {
+      const int slot = ci % R;
+      const int ahead = nch - 1 - ci;
+      wait_chunks<PC, R>(ahead < R - 1 ? ahead : R - 1);
+      if (ci == 0) {
+        u32x4 qraw[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) qraw[c] = ds_read_b128(qlds + c16 * D * 2 + (4 * c + g) * 16);
+        lds_wait_all();
 #pragma unroll
         for (int c = 0; c < NC; ++c) {
-          kr[j][c] = kn[j][c];
-          vr[j][c] = vn[j][c];
+          lds_ready(qraw[c]);
+          qop[c] = c16 < G ? __builtin_bit_cast(V8, qraw[c]) : zero8<DT>();
         }
+      }
+      compute_chunk(ci, slot);
+      const int nx = ci + R;
+      if (nx < nch) {
+        // The slot's LDS reads are done (their results were used above).
+        if constexpr (BIG) {
+          const int64_t a = tile_block(2 * nx);
+          issue_chunk(nx, slot, a, 2 * nx + 1 < wtiles ? tile_block(2 * nx + 1) : a);
+        } else {
+          issue_chunk(nx, slot, 0, 0);
+        }
+      }
     }
   }
-  l_run = group4_sum(l_run);
+  l_run = group4_sum_swap(l_run);
 
-  // Merge the waves' (max, sum, O) through LDS.
-  bad = __syncthreads_or(bad);
-  // Rows (wave, head) padded to RED_LD floats and written a float4 at a
-  // time: the 16 head lanes of one store then start on 16 different 4-bank
-  // groups instead of one bank (a 16-way conflict: ~0.4 us of a 13 us call).
+  // Merge the waves' (max, sum, O) through LDS.  Each wave writes its block
+  // into the first slot of its own ring (no other wave touches that memory,
+  // so no barrier is needed before the writes): rows (head) padded to RED_LD
+  // floats and written a float4 at a time, so the 16 head lanes of a store
+  // start on 16 different 4-bank groups; then the maxima, the sums and the
+  // wave's invalid-block flag.  One barrier hands the blocks over.
   constexpr int RED_LD = Cfg::RED_LD;
-  float* red_o = reinterpret_cast<float*>(smem);
-  float* red_m = red_o + W * 16 * RED_LD;
-  float* red_l = red_m + W * 16;
+  static_assert(16 * RED_LD * 4 + 33 * 4 <= Cfg::SLOT_B, "a wave's reduce block fits its first ring slot");
+  auto red_o = [&](int ww) { return reinterpret_cast<float*>(smem + ww * Cfg::WAVE_B); };
+  auto red_m = [&](int ww) { return red_o(ww) + 16 * RED_LD; };
+  auto red_l = [&](int ww) { return red_o(ww) + 16 * RED_LD + 16; };
+  auto red_bad = [&](int ww) { return reinterpret_cast<int*>(red_o(ww) + 16 * RED_LD + 32); };
+  {
+    float* ro = red_o(w);
 #pragma unroll
-  for (int n = 0; n < NN; ++n)
-    *reinterpret_cast<floatx4*>(red_o + (w * 16 + c16) * RED_LD + 16 * n + 4 * g) = acc[n];
-  if (g == 0) {
-    red_m[w * 16 + c16] = m_run;
-    red_l[w * 16 + c16] = l_run;
+    for (int n = 0; n < NN; ++n) *reinterpret_cast<floatx4*>(ro + c16 * RED_LD + 16 * n + 4 * g) = acc[n];
+    if (g == 0) {
+      red_m(w)[c16] = m_run;
+      red_l(w)[c16] = l_run;
+    }
+    const int wave_bad = __builtin_amdgcn_ballot_w64(bad != 0) != 0;
+    if (lane == 0) *red_bad(w) = wave_bad;
   }
   __syncthreads();
+  bad = 0;
+#pragma unroll
+  for (int ww = 0; ww < W; ++ww) bad |= *red_bad(ww);
 
   const int slot_words = p.slot_words;
   const __amdgpu_buffer_rsrc_t pr =
@@ -495,16 +705,16 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
     const int col = it / (D / 4), d4 = it % (D / 4);
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, red_m[ww * 16 + col]);
+    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, red_m(ww)[col]);
     float lsum = 0.f;
     floatx4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < W; ++ww) {
-      const float mw = red_m[ww * 16 + col];
+      const float mw = red_m(ww)[col];
       if (mw != -INFINITY) {
         const float sc = fast_exp2(mw - M);
-        lsum += red_l[ww * 16 + col] * sc;
-        o += *reinterpret_cast<const floatx4*>(red_o + (ww * 16 + col) * RED_LD + 4 * d4) * sc;
+        lsum += red_l(ww)[col] * sc;
+        o += *reinterpret_cast<const floatx4*>(red_o(ww) + col * RED_LD + 4 * d4) * sc;
       }
     }
     if (bad) {
@@ -542,17 +752,16 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
   if (tid == 0) __hip_atomic_store(&p.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <class DT, int D, int W, int CH, class BTI, bool BIG>
+template <class DT, int D, int W, int R, class BTI, bool BIG>
 __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) char smem[DecodeCfg<D, W, CH>::LDS];
-  __shared__ int64_t later_lds[BIG ? W * 64 : 1];
+  __shared__ __attribute__((aligned(16))) char smem[DecodeCfg<D, W, R>::LDS];
   __shared__ int s_merger;
   // The first item loads together with the plan's item count: the grid
   // never exceeds the plan's capacity, so the read is in bounds either way.
   uint32_t idx = blockIdx.x;
   u32x4 r0, r1;
-  WaveBlocks<W, CH> ib;
-  load_item<W, CH>(p, idx, r0, r1, ib);
+  WaveBlocks ib;
+  load_item(p, idx, r0, r1, ib);
   const uint32_t n_hdr = p.plan_hdr->n_items;
   // Both scalar loads are in flight before either is waited for (the
   // compiler would otherwise sink the item's load below the count check:
@@ -561,9 +770,14 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
                "s"(ib.id[4]), "s"(ib.id[5]), "s"(ib.id[6]), "s"(ib.id[7]));
   const uint32_t n_items = n_hdr < p.item_cap ? n_hdr : static_cast<uint32_t>(p.item_cap);
   while (idx < n_items) {
-    decode_item<DT, D, W, CH, BTI, BIG>(p, idx, r0, r1, ib, smem, later_lds, s_merger);
+    decode_item<DT, D, W, R, BTI, BIG>(p, idx, r0, r1, ib, smem, s_merger);
+    // Everything the item issued has completed, and the compiler's wait-count
+    // pass sees that through this builtin: it then carries no pending loads
+    // around the loop, so it puts no wait of its own into the next item,
+    // where any vmcnt wait would also drain that item's K/V loads.
+    __builtin_amdgcn_s_waitcnt(0);
     idx += gridDim.x;
-    if (idx < n_items) load_item<W, CH>(p, idx, r0, r1, ib);
+    if (idx < n_items) load_item(p, idx, r0, r1, ib);
     __syncthreads();  // the next item reuses the LDS
   }
 }
@@ -618,14 +832,6 @@ struct PrefillCfg {
   static_assert(WC * NF * 64 * 4 <= RING, "merge buffer fits the ring");
 };
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
-
-// Address-space views for global_load_lds (global source, LDS destination).
-typedef __attribute__((address_space(1))) void* gbl_void_ptr;
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
-__device__ __forceinline__ int k_swz(int key) { return key & 7; }
-__device__ __forceinline__ int v_swz(int key) { return (key & 3) << 1; }
 
 // Wait until at most N of this wave's vector-memory operations are pending,
 // drain its LDS operations, then barrier.  Written as one asm statement so the
@@ -1114,11 +1320,15 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
 // 16-column tiles per prefill wave (columns per workgroup = 64 * kPrefillTiles).
 constexpr int kPrefillTiles = 2;
 
-// Decode launch shape: kDecodeWaves waves per workgroup, each moving
-// decode_chunk<D> tokens (16 KiB of K+V) per step.
+// Decode launch shape: kDecodeWaves waves per workgroup, each with a ring of
+// decode_ring<D> chunk slots (16 KiB of LDS per wave at head_dim 64, 32 KiB
+// at 128).  Two chunks in flight per wave measured faster than three or
+// four (c2 12.43 / 12.64 / 12.80 us per call): the fewer bytes each wave
+// has queued, the sooner its first chunk lands and its compute overlaps
+// the rest of the stream.
 constexpr int kDecodeWaves = 4;
 template <int D>
-constexpr int decode_chunk() { return D == 64 ? 64 : 32; }
+constexpr int decode_ring() { return 2; }
 
 // Words of one decode split-K slot: G rows of D outputs, then G (max, sum)
 // pairs, padded to 16 bytes.
@@ -1214,7 +1424,7 @@ DecodePlanArgs plan_args(void* plan, int64_t item_cap, const void* block_tables,
   a.bt_stride = bt_stride;
   a.bt64 = bt64 ? 1 : 0;
   a.bs_shift = bs_shift;
-  a.tiles_per_step = (head_dim == 64 ? decode_chunk<64>() : decode_chunk<128>()) / 16;
+  a.tiles_per_step = 2;  // a 32-token chunk; the carried ids are wave w's tiles 0..7 either way
   a.seq_lens = seq_lens;
   a.sl64 = sl64 ? 1 : 0;
   a.qsl = qsl;
@@ -1266,17 +1476,17 @@ hipError_t launch_decode_rows(AttnParams& p, const DecodePlanArgs* build, int gr
     if (e != hipSuccess) return e;
   }
   void* args[] = {&p};
-  constexpr int W = kDecodeWaves, CH = decode_chunk<D>();
+  constexpr int W = kDecodeWaves, R = decode_ring<D>();
   // The block-table width is a template argument so table loads need no
   // per-lane branch.
   // Block size >= 16 (the item carries block ids) and the table's index
   // width select the kernel at compile time.
   const void* dk =
       p.inline_blocks
-          ? (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, true>)
-                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, true>))
-          : (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int64_t, false>)
-                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, CH, int32_t, false>));
+          ? (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, R, int64_t, true>)
+                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, R, int32_t, true>))
+          : (p.bt64 ? reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, R, int64_t, false>)
+                    : reinterpret_cast<const void*>(&paged_decode_kernel<DT, D, W, R, int32_t, false>));
   return hipLaunchKernel(dk, dim3(grid), dim3(W * 64), args, 0, stream);
 }
 
