@@ -703,19 +703,28 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
   // One float4 of the workgroup's output per thread and round: (head col, dims 4*d4..+3).
   for (int it = tid; it < G * (D / 4); it += THREADS) {
     const int col = it / (D / 4), d4 = it % (D / 4);
+    // Every read first, then branch-free arithmetic: a wave without tokens
+    // (max -inf) contributes nothing.
+    float mw[W], lw[W];
+    floatx4 ow[W];
+#pragma unroll
+    for (int ww = 0; ww < W; ++ww) {
+      mw[ww] = red_m(ww)[col];
+      lw[ww] = red_l(ww)[col];
+      ow[ww] = *reinterpret_cast<const floatx4*>(red_o(ww) + col * RED_LD + 4 * d4);
+    }
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, red_m(ww)[col]);
+    for (int ww = 0; ww < W; ++ww) M = fmaxf(M, mw[ww]);
     float lsum = 0.f;
     floatx4 o = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ww = 0; ww < W; ++ww) {
-      const float mw = red_m(ww)[col];
-      if (mw != -INFINITY) {
-        const float sc = fast_exp2(mw - M);
-        lsum += red_l(ww)[col] * sc;
-        o += *reinterpret_cast<const floatx4*>(red_o(ww) + col * RED_LD + 4 * d4) * sc;
-      }
+      const bool on = mw[ww] != -INFINITY;
+      const float sc = on ? fast_exp2(mw[ww] - M) : 0.f;
+      lsum += on ? lw[ww] * sc : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[r] += on ? ow[ww][r] * sc : 0.f;
     }
     if (bad) {
       lsum = NAN;
@@ -1413,6 +1422,17 @@ int current_device_cus() {
   return n;
 }
 
+// CUs a decode plan is sized for.  The decode rows of a mixed batch run
+// beside the prefill kernel (on the caller's aux stream), and a workgroup of
+// either holds most of a CU's LDS, so their plan takes a quarter of the CUs
+// and leaves the rest to the prefill column blocks.
+int plan_cus(bool decode_only) {
+  const int n = current_device_cus();
+  if (decode_only) return n;
+  const int q = n / 4;
+  return q < 1 ? 1 : q;
+}
+
 DecodePlanArgs plan_args(void* plan, int64_t item_cap, const void* block_tables, int64_t bt_stride, int bt64,
                          int bs_shift, const void* seq_lens, int sl64, const void* qsl, int qsl64,
                          int is_decode_only, int num_seqs, int num_kv_heads, int64_t max_ctx, int head_dim,
@@ -1685,7 +1705,7 @@ extern "C" int ns_paged_decode_plan(void* plan, size_t plan_bytes, const void* b
   const int64_t max_ctx = ctx_plan < table_tokens ? ctx_plan : table_tokens;
   DecodeShape d = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, kPlanCUs);
   if (plan_bytes < plan_bytes_needed(num_seqs, d.item_cap)) return NS_ERR_WORKSPACE;
-  d = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, current_device_cus());
+  d = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, plan_cus(is_decode_only != 0));
   const DecodePlanArgs a = plan_args(plan, d.item_cap, block_tables, block_table_stride, block_tables_is_int64,
                                      bs_shift, seq_lens, seq_lens_is_int64, query_start_loc,
                                      query_start_loc_is_int64, is_decode_only, num_seqs, num_kv_heads, max_ctx,
@@ -1805,7 +1825,7 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
     workspace_bytes = kNoallocScratchBytes;
   }
   if (!workspace || workspace_bytes < wl.total) return NS_ERR_WORKSPACE;
-  dshape = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, current_device_cus());
+  dshape = decode_shape(num_seqs, num_kv_heads, max_ctx, head_dim, plan_cus(is_decode_only != 0));
 
   AttnParams p;
   p.out = static_cast<char*>(out);
