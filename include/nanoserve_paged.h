@@ -148,7 +148,10 @@ int ns_rope_reshape_and_cache(void* q_out, const void* query,
  * and at most 1024.
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16.  N must be a multiple of 16, K and
  * group_size multiples of 32 with K a multiple of group_size; qweight 16-byte
- * aligned, out 8-byte aligned.
+ * aligned, out 8-byte aligned.  Up to 128 rows one kernel dequantises each
+ * weight tile per 16 or 64 tokens; above, a tiled GEMM (K a multiple of 64,
+ * no norm_weight, bias 8-byte and zeros 4-byte aligned; otherwise the first
+ * kernel) dequantises it once per 128 or 256 tokens.
  */
 int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
                    const void* qweight, const void* scales, const void* zeros, const void* bias,
@@ -157,13 +160,15 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
 
 /*
  * ns_int4_linear_splitk -- ns_int4_linear with the K loop of long-K layers
- * split over several workgroups per 16-feature tile (down_proj of
- * Qwen2.5-0.5B: N = 896 is 56 tiles, too few for the device, each walking
- * K = 4864).  Same operands, epilogues and prologue as ns_int4_linear; the
- * fp32 partial sums of each split go to `workspace` and the last split of a
- * tile adds them in split order (deterministic) and runs the epilogue.  The
- * split count (up to 4) keeps tiles x splits within 256 workgroups, so it
- * depends on N, K and the number of token tiles.  Same replacement as ns_int4_linear (reference
+ * split over several workgroups per output tile (down_proj of
+ * Qwen2.5-0.5B: N = 896 is 56 tiles of 16 features, or 14 of 64, too few for
+ * the device, each walking K = 4864).  Same operands, epilogues and prologue
+ * as ns_int4_linear; the fp32 partial sums of each split go to `workspace`
+ * and the last split of a tile adds them in split order (deterministic) and
+ * runs the epilogue.  The split count (up to 4) keeps tiles x splits within
+ * 256 workgroups up to 128 tokens (register-dequant kernel) and within 512
+ * above (tiled GEMM), so it depends on N, K and the number of token tiles.
+ * Same replacement as ns_int4_linear (reference
  * nanoserve/quant.py:157-158).  workspace: 256-byte aligned,
  * ns_int4_linear_splitk_workspace_size(M, N, K) bytes, zeroed once before
  * first use; every call leaves its arrival counters at zero.  Calls that

@@ -24,6 +24,8 @@
 // way for both operands, so the sum is unchanged).  The same lane reads the
 // matching 8 x values per step for each column tile.  The result D[n][m]
 // lands as four consecutive features of one token per lane: one 8-byte store.
+#include <algorithm>
+
 #include "ns_common.h"
 
 namespace ns {
@@ -107,6 +109,44 @@ __device__ __forceinline__ typename DT::vec8 dequant8(uint32_t word, float zero,
   for (int e = 0; e < 8; ++e) {
     const float q = static_cast<float>((word >> (4 * e)) & 0xFu);
     a[e] = to_model<DT>((q - zero) * scale);
+  }
+  return a;
+}
+
+// dequant8 in fewer VALU operations, with the same result.  The codes of
+// byte i (k = 2i, 2i+1) become the f16 pair (1024 + q) by one byte permute
+// and one and-or (1024 + q is exact in f16 for q < 1024); one packed f16 add
+// of `zbias` = the pair (-(1024 + z), -(1024 + z)) leaves q - z, exact (an
+// integer in [-255, 15]); v_fma_mix_f32 then forms (q - z) * scale in fp32
+// with one rounding (f16 operand times f32 operand, plus 0): the float32
+// product of dequantize_int4, which the model-dtype conversion rounds.
+__device__ __forceinline__ uint32_t zero_bias_f16x2(uint32_t zero) { return (0xE400u | zero) * 0x00010001u; }
+
+// `magic` holds 0x64006400 in a VGPR (opaque to the compiler, so the mask
+// and this constant fit one v_and_or_b32: VOP3 takes no second literal).
+__device__ __forceinline__ uint32_t f16_magic_pair() {
+  uint32_t m = 0x64006400u;
+  asm("" : "+v"(m));
+  return m;
+}
+
+template <class DT>
+__device__ __forceinline__ typename DT::vec8 dequant8_mix(uint32_t word, uint32_t zbias, float scale, uint32_t magic) {
+  typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+  const uint32_t hi = word >> 4;
+  typename DT::vec8 a;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bytes [byte i of word, 0, byte i of word >> 4, 0]: the low nibbles are
+    // the codes of k = 2i and 2i + 1.
+    const uint32_t sel = static_cast<uint32_t>(i) | 0x0C00u | (static_cast<uint32_t>(4 + i) << 16) | 0x0C000000u;
+    const uint32_t t = (__builtin_amdgcn_perm(hi, word, sel) & 0x000F000Fu) | magic;
+    const uint32_t d = __builtin_bit_cast(uint32_t, __builtin_bit_cast(half2_t, t) + __builtin_bit_cast(half2_t, zbias));
+    float lo, up;
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(lo) : "v"(d), "v"(scale));
+    asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(up) : "v"(d), "v"(scale));
+    a[2 * i] = static_cast<typename DT::T>(lo);
+    a[2 * i + 1] = static_cast<typename DT::T>(up);
   }
   return a;
 }
@@ -641,6 +681,337 @@ hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream, int
 
 bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q) % a == 0; }
 
+// --------------------------------------------------------------------------
+// Token counts of prefill chunks (M above kGemmMinRows): a tiled GEMM whose
+// waves dequantise weight codes in registers, straight into the MFMA operand
+// layout, and reuse each dequantised fragment over many tokens.  The fused
+// kernel above dequantises a weight tile once per 16- or 64-token tile, which
+// at prefill sizes makes the dequantisation, not the MFMA, its bound.
+//
+// Workgroup: 4 waves, BN features x BM tokens; WN waves side by side along
+// the features and 4/WN along the tokens, wave (wn, wm) computing WF features
+// x WT tokens as MFMA 16x16x32 tiles (A = W rows, B = x^T), so a lane ends
+// with four consecutive features of one token, as in the fused kernel, and
+// the epilogues are the same.  Each 64-wide K step's x tile, weight codes,
+// scales and zero-point words go from HBM into LDS by global_load_lds
+// through a ring of NST stages.  Within a step, lane group g of the MFMA
+// operands carries k = 16g + 8j .. +7 in sub-step j (a permutation of the 64
+// k, the same for both operands), so a lane's two sub-steps of one weight
+// row are one 8-byte word pair of codes.  The lane dequantises them with
+// dequantize_int4's arithmetic (quant.py:83-95) one step ahead of the MFMAs
+// that use them (software pipeline: step s+1's dequantisation and step s's
+// MFMAs are independent work in one block).  x rows in LDS are 128 bytes
+// with 16-byte unit c of row r at c ^ (r & 7), so the operand reads of a
+// wave spread over the banks.  Every wait for the ring is an explicit vmcnt
+// (the loads are issued from asm, invisible to the compiler's wait-count
+// pass).
+//
+// Split-K (gridDim.z = S > 1, long-K layers with few tiles): split z walks
+// steps [z*steps/S, (z+1)*steps/S), publishes its fp32 partial tile to the
+// workspace and counts its arrival; the last split of the tile adds all S
+// partials in split order and applies the epilogue.
+// --------------------------------------------------------------------------
+constexpr int64_t kGemmMinRows = 128;  // the fused kernel takes M up to here
+namespace gemm {
+constexpr int BK = 64;
+constexpr int WAVES = 4, THREADS = WAVES * 64;
+constexpr int ROW_B = BK * 2;  // one LDS row of x: 64 k in the model dtype
+// BM tokens x BN features per workgroup; NST stages in the load ring; WN
+// waves side by side along the features (4 / WN along the tokens).
+template <int BM, int BN, int NST, int WN>
+struct Cfg {
+  static constexpr int X_B = BM * ROW_B;       // x tile of a stage
+  static constexpr int C_B = BN * BK / 2;      // weight codes of a stage (32 bytes a row)
+  static constexpr int SZ_B = BN * 2 * 4;      // a scale (or zero-point word) per row and 32-k half
+  static constexpr int STAGE_B = X_B + C_B + 2 * SZ_B;
+  static constexpr int LDS = NST * STAGE_B;
+  static constexpr int X_DMA = X_B / 1024 / WAVES;  // 16-byte global_load_lds per wave
+  // Per wave and step: x loads, one code load, one scale and one zero-point
+  // load (waves past the table's size repeat an earlier wave's loads, the
+  // same bytes to the same LDS words, so every wave counts the same).
+  static constexpr int PS = X_DMA + 3;
+  static constexpr int WM = WAVES / WN;
+  static constexpr int WF = BN / WN, WT = BM / WM;  // features and tokens of one wave
+  static constexpr int FT = WF / 16, TT = WT / 16;  // 16-row MFMA tiles per wave: features, tokens
+  static_assert(X_B % (1024 * WAVES) == 0 && C_B % 1024 == 0 && SZ_B % 256 == 0, "whole loads per wave");
+  static_assert(C_B <= 1024 * WAVES && SZ_B <= 256 * WAVES, "one code, scale and zero load per lane cover a step");
+  static_assert(NST >= 3, "the loop dequantises one step ahead of its MFMAs");
+  static_assert(LDS <= 80 * 1024, "two workgroups fit one CU's LDS");
+};
+// Split-K: at most this many tiles split (their arrival counters lie at the
+// start of the workspace).
+constexpr int kMaxSplitTiles = 256;
+}  // namespace gemm
+
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <class DT, int BM, int BN, int NST, int WN>
+__global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearParams p) {
+  using namespace gemm;
+  using C = Cfg<BM, BN, NST, WN>;
+  using T = typename DT::T;
+  using V8 = typename DT::vec8;
+  using V4 = typename DT::vec4;
+  constexpr int ESZ = sizeof(T);
+  constexpr int TT = C::TT, FT = C::FT;
+  __shared__ __attribute__((aligned(16))) char smem[C::LDS];
+  auto xst = [&](int st) { return smem + st * C::STAGE_B; };
+  auto cst = [&](int st) { return smem + st * C::STAGE_B + C::X_B; };
+  auto sst = [&](int st) { return smem + st * C::STAGE_B + C::X_B + C::C_B; };
+  auto zst = [&](int st) { return smem + st * C::STAGE_B + C::X_B + C::C_B + C::SZ_B; };
+
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = w % WN, wm = w / WN;
+  // Grid: feature tiles along x (consecutive workgroups share one x row
+  // block, spread over the XCDs by the round-robin dispatch: an XCD-local
+  // renumbering measured slower), token tiles along y, K splits along z.
+  const int gx = gridDim.x, S = gridDim.z, z = blockIdx.z;
+  const int tile = blockIdx.y * gx + blockIdx.x;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int steps = p.K / BK;
+  const int s0 = z * steps / S, s1 = (z + 1) * steps / S;
+
+  // Loader roles of this lane (rows past N repeat the last one, never stored).
+  const int cu = (w * 64 + lane) % (C::C_B / 16);  // 16-byte code unit: row cu/2, half cu&1
+  const int8_t* crow = reinterpret_cast<const int8_t*>(p.qweight) +
+                       static_cast<int64_t>(min(n0 + (cu >> 1), p.N - 1)) * (p.K / 2) + 16 * (cu & 1);
+  const int se = (w * 64 + lane) % (C::SZ_B / 4);  // scale entry: row se/2, 32-k half se&1
+  const int64_t sidx = static_cast<int64_t>(min(n0 + (se >> 1), p.N - 1)) * p.groups;
+  // This lane's operand rows: features WF wn + 16 fi + c16 of the tile.
+  int64_t zbase[FT];
+#pragma unroll
+  for (int fi = 0; fi < FT; ++fi)
+    zbase[fi] = static_cast<int64_t>(min(n0 + C::WF * wn + 16 * fi + c16, p.N - 1)) * p.groups;
+
+  auto dma = [&](int s, int st) {
+#pragma unroll
+    for (int u = 0; u < C::X_DMA; ++u) {
+      const int i = w * C::X_DMA + u;
+      const int unit = i * 64 + lane;
+      const int row = unit >> 3, pos = unit & 7;
+      const int m = min(m0 + row, p.M - 1);  // rows past M repeat the last one (never stored)
+      dma_lds16(p.x + (static_cast<int64_t>(m) * p.x_stride + BK * s + 8 * (pos ^ (row & 7))) * ESZ,
+                xst(st) + i * 1024);
+    }
+    dma_lds16(crow + (BK / 2) * s, cst(st) + (w * 1024) % C::C_B);
+    const int gi = (BK * s + 32 * (se & 1)) / p.group_size;
+    dma_lds4(p.scales + sidx + gi, sst(st) + (w * 256) % C::SZ_B);
+    // The aligned word holding the zero point (the table is 4-byte aligned and
+    // N * groups a multiple of 16, so the word lies inside it).
+    dma_lds4(p.zeros + ((sidx + gi) & ~int64_t{3}), zst(st) + (w * 256) % C::SZ_B);
+  };
+
+  floatx4 acc[FT][TT];
+#pragma unroll
+  for (int fi = 0; fi < FT; ++fi)
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti) acc[fi][ti] = floatx4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t magic = f16_magic_pair();
+
+  auto stage = [&](int s) { return (s - s0) % NST; };
+  // Wait until at most n whole steps of this wave's loads are in flight.
+  auto wait_steps = [&](int n) {
+    if (n >= 2) wait_vm<2 * C::PS>();
+    else if (n == 1) wait_vm<C::PS>();
+    else wait_vm<0>();
+  };
+  // The A operands of step s: this lane's codes of rows WF wn + 16 fi + c16,
+  // k of the step in one group per lane, dequantised into both sub-steps.
+  auto dequant_step = [&](int s, V8 (&a)[FT][2]) {
+    const int st = stage(s);
+    const int gi = (BK * s + 16 * g) / p.group_size;
+#pragma unroll
+    for (int fi = 0; fi < FT; ++fi) {
+      const int r = C::WF * wn + 16 * fi + c16;
+      const u32x2 words = *reinterpret_cast<const u32x2*>(cst(st) + 32 * r + 8 * g);
+      const float scale = *reinterpret_cast<const float*>(sst(st) + 4 * (2 * r + (g >> 1)));
+      const uint32_t zword = *reinterpret_cast<const uint32_t*>(zst(st) + 4 * (2 * r + (g >> 1)));
+      const uint32_t zb = zero_bias_f16x2((zword >> (8 * ((zbase[fi] + gi) & 3))) & 0xFFu);
+      a[fi][0] = dequant8_mix<DT>(words[0], zb, scale, magic);
+      a[fi][1] = dequant8_mix<DT>(words[1], zb, scale, magic);
+    }
+  };
+  // The MFMAs of step s: A from registers, B (x rows of this wave's tokens)
+  // read from the step's stage as each token tile's turn comes.
+  auto mfma_step = [&](int s, const V8 (&a)[FT][2]) {
+    const char* xt = xst(stage(s));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti) {
+        const int row = C::WT * wm + 16 * ti + c16;
+        const V8 b = *reinterpret_cast<const V8*>(xt + row * ROW_B + (((2 * g + j) ^ (c16 & 7)) << 4));
+#pragma unroll
+        for (int fi = 0; fi < FT; ++fi) acc[fi][ti] = mfma16x16x32(DT{}, a[fi][j], b, acc[fi][ti]);
+      }
+    }
+  };
+
+  // Software pipeline: iteration s dequantises step s+1 while the MFMAs of
+  // step s run (independent work in one block, so the two interleave), with
+  // the loads of up to NST-2 later steps in flight.
+#pragma unroll
+  for (int k = 0; k < NST - 1; ++k)
+    if (s0 + k < s1) dma(s0 + k, k);
+  wait_steps(min(s1 - 1 - s0, NST - 2));
+  __syncthreads();
+  V8 acur[FT][2];
+  dequant_step(s0, acur);
+  for (int s = s0; s < s1 - 1; ++s) {
+    // Step s+1's loads have landed (those up to step s+NST-2 may fly); past
+    // the barrier every wave is done with step s-1, whose stage takes step
+    // s+NST-1.
+    wait_steps(min(s1 - 1, s + NST - 2) - (s + 1));
+    __syncthreads();
+    if (s + NST - 1 < s1) dma(s + NST - 1, stage(s + NST - 1));
+    V8 anext[FT][2];
+    dequant_step(s + 1, anext);
+    mfma_step(s, acur);
+#pragma unroll
+    for (int fi = 0; fi < FT; ++fi) {
+      acur[fi][0] = anext[fi][0];
+      acur[fi][1] = anext[fi][1];
+    }
+  }
+  mfma_step(s1 - 1, acur);
+
+  if (S > 1) {
+    // Publish this split's sums, count the arrival; the last split of the
+    // tile adds all S partials in split order (its own included, so the
+    // result does not depend on which split came last) and resets the counter.
+    __shared__ unsigned last_arrival;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(p.part, static_cast<short>(0), p.part_bytes, kBufferWord3);
+    auto off = [&](int zz, int fi, int ti) { return ((((tile * S + zz) * WAVES + w) * FT + fi) * TT + ti) * 1024 + lane * 16; };
+#pragma unroll
+    for (int fi = 0; fi < FT; ++fi)
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[fi][ti]), rs, off(z, fi, ti), 0, kSc1);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are acknowledged
+    __syncthreads();                     // ... by every wave
+    if (tid == 0)
+      last_arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                     static_cast<unsigned>(S - 1);
+    __syncthreads();
+    if (!last_arrival) return;
+#pragma unroll
+    for (int fi = 0; fi < FT; ++fi)
+#pragma unroll
+      for (int ti = 0; ti < TT; ++ti) {
+        floatx4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int zz = 0; zz < S; ++zz)
+          sum += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off(zz, fi, ti), 0, kSc1));
+        acc[fi][ti] = sum;
+      }
+    if (tid == 0) __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  // D[4g + r][c16] of tile (fi, ti): features nf .. nf+3 of token m, rounded
+  // where the reference's separate tensor ops round (as the fused kernel).
+#pragma unroll
+  for (int fi = 0; fi < FT; ++fi) {
+    const int nf = n0 + C::WF * wn + 16 * fi + 4 * g;
+    if (nf >= p.N) continue;
+    float bias[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+      const V4 b4 = *reinterpret_cast<const V4*>(static_cast<const T*>(p.bias) + nf);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bias[r] = from_model<DT>(b4[r]);
+    }
+#pragma unroll
+    for (int ti = 0; ti < TT; ++ti) {
+      const int m = m0 + C::WT * wm + 16 * ti + c16;
+      if (m >= p.M) continue;
+      float y[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) y[r] = from_model<DT>(to_model<DT>(acc[fi][ti][r] + bias[r]));
+      if (p.epilogue == NS_EPILOGUE_SILU_MUL) {
+        T o[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float act = from_model<DT>(to_model<DT>(silu_f32(y[2 * h])));
+          o[h] = to_model<DT>(act * y[2 * h + 1]);
+        }
+        // Outputs nf/2 and nf/2 + 1 (nf a multiple of 4): one 4-byte store.
+        T* dst = static_cast<T*>(p.out) + static_cast<int64_t>(m) * (p.N / 2) + nf / 2;
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_bit_cast(uint16_t, o[0]) |
+                                            (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, o[1])) << 16);
+        continue;
+      }
+      V4 o;
+      if (p.epilogue == NS_EPILOGUE_RESIDUAL) {
+        const V4 res = *reinterpret_cast<const V4*>(static_cast<const T*>(p.residual) + static_cast<int64_t>(m) * p.N + nf);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r] + from_model<DT>(res[r]));
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = to_model<DT>(y[r]);
+      }
+      *reinterpret_cast<V4*>(static_cast<T*>(p.out) + static_cast<int64_t>(m) * p.N + nf) = o;
+    }
+  }
+}
+
+struct GemmShape {
+  int bm, bn, nst, wn, splits;
+};
+
+// Tile shape and split count of a GEMM call, from measurements on MI355X
+// (fp16, Qwen2.5-0.5B projections, graph-replayed).  128 x 128 tiles when
+// they still give two workgroups per CU (gate|up from 1024 tokens: 44.8 /
+// 66.3 us at 1024 / 2048 tokens against 46.9 / 86.7 with 64 x 128 tiles);
+// 128-token x 64-feature tiles for long-K layers with enough of them
+// (down_proj at 2048 tokens, split twice: 49.1 us against 53.9 with 64 x 128
+// tiles); 64 x 64 tiles otherwise, the most workgroups for short calls (qkv /
+// o / down at 256 tokens: 10.4 / 10.8 / 21.6 us, against 13.8 / 14.8 / 30.7
+// with 64 x 128).  Tiles that cannot fill the device split long K loops
+// (at least 8 steps a split) when the caller gave a workspace.
+GemmShape gemm_shape(int64_t M, int N, int K, bool can_split) {
+  auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+  GemmShape s{64, 64, 4, 4, 1};
+  if (tiles(128, 128) >= 512) s = {128, 128, 3, 4, 1};
+  else if (K >= 2048 && tiles(128, 64) >= 200) s = {128, 64, 3, 4, 1};
+  const int64_t t = tiles(s.bm, s.bn);
+  if (can_split && t * 2 <= 512 && t <= gemm::kMaxSplitTiles) {
+    const int steps = K / gemm::BK;
+    s.splits = static_cast<int>(std::min<int64_t>(std::min(512 / t, int64_t{4}), steps / 8));
+    if (s.splits < 1) s.splits = 1;
+  }
+  return s;
+}
+
+int64_t gemm_part_bytes(int64_t M, int N, const GemmShape& s) {
+  if (s.splits <= 1) return 0;
+  const int64_t tiles = ((M + s.bm - 1) / s.bm) * ((N + s.bn - 1) / s.bn);
+  return tiles * s.splits * static_cast<int64_t>(s.bm) * s.bn * 4;
+}
+
+// Instantiated tile configurations: (BM, BN, NST, WN).
+#define NS_INT4_GEMM_CONFIGS(X) \
+  X(128, 128, 3, 4)             \
+  X(128, 64, 3, 4)              \
+  X(64, 64, 4, 4)
+
+template <class DT>
+hipError_t launch_int4_gemm(const Int4LinearParams& p, const GemmShape& s, hipStream_t stream) {
+  void* args[] = {const_cast<Int4LinearParams*>(&p)};
+  const void* fn = nullptr;
+#define NS_PICK(BM_, BN_, NST_, WN_) \
+  if (s.bm == BM_ && s.bn == BN_ && s.nst == NST_ && s.wn == WN_) \
+    fn = reinterpret_cast<const void*>(&int4_gemm_kernel<DT, BM_, BN_, NST_, WN_>);
+  NS_INT4_GEMM_CONFIGS(NS_PICK)
+#undef NS_PICK
+  if (!fn) return hipErrorInvalidValue;
+  const dim3 grid(static_cast<unsigned>((p.N + s.bn - 1) / s.bn), static_cast<unsigned>((p.M + s.bm - 1) / s.bm),
+                  static_cast<unsigned>(s.splits));
+  return hipLaunchKernel(fn, grid, dim3(gemm::THREADS), args, 0, stream);
+}
+
 // Whole-weight dequantisation for large token counts, where a library GEMM on
 // the model-dtype weight beats re-dequantising each weight tile per token
 // tile.  One thread turns one 32-bit word (8 codes) into 16 bytes of weights,
@@ -666,28 +1037,39 @@ namespace ns {
 namespace {
 
 // Split-K workspace: a fixed region of u32 arrival counters (one per tile,
-// zero between calls), then the partial sums, 16 bytes per lane, tile and
-// split.  The region has the same size for every M: a tile only splits when
-// 2 * tiles <= 256, so at most 128 counters exist, and the partials of any
-// call start past every counter any other call may use.  One workspace can
-// therefore serve calls of every token count in turn (a layer's decode steps
-// change M from step to step) without a call's partial sums landing on
-// another call's counters.
-constexpr int64_t kSplitkMaxTiles = 128;
-constexpr int64_t kSplitkCounterBytes = kSplitkMaxTiles * 4;
+// zero between calls), then the partial sums.  The region has the same size
+// for every M: the fused kernel only splits when 2 * tiles <= 256 and the
+// GEMM when tiles <= gemm::kMaxSplitTiles, so at most 256 counters exist,
+// and the partials of any call start past every counter any other call may
+// use.  One workspace can therefore serve calls of every token count in turn
+// (a layer's decode steps change M from step to step) without a call's
+// partial sums landing on another call's counters.
+constexpr int64_t kSplitkCounterBytes = gemm::kMaxSplitTiles * 4;
 
 struct SplitkLayout {
   int splits;
   int64_t counter_bytes, part_bytes;
 };
 
+// Token counts above kGemmMinRows take the GEMM (when K is a whole number of
+// its steps), the rest the fused kernel with 16 bytes of partials per lane,
+// tile and split.
 SplitkLayout splitk_layout(int64_t M, int N, int K) {
-  const int mt = M <= 64 ? 16 : 64;
-  const int64_t tiles = static_cast<int64_t>(N / 16) * ((M + mt - 1) / mt);
-  SplitkLayout l;
-  l.splits = M > 0 ? splitk_for(N, K, (M + mt - 1) / mt) : 1;
+  SplitkLayout l{1, 0, 0};
+  if (M <= 0) return l;
+  if (M > kGemmMinRows) {
+    if (K % gemm::BK == 0) {
+      const GemmShape gs = gemm_shape(M, N, K, true);
+      l.splits = gs.splits;
+      l.part_bytes = gemm_part_bytes(M, N, gs);
+    }
+  } else {
+    const int mt = M <= 64 ? 16 : 64;
+    const int64_t tiles = static_cast<int64_t>(N / 16) * ((M + mt - 1) / mt);
+    l.splits = splitk_for(N, K, (M + mt - 1) / mt);
+    l.part_bytes = l.splits > 1 ? tiles * l.splits * (mt / 16) * 64 * 16 : 0;
+  }
   l.counter_bytes = l.splits > 1 ? kSplitkCounterBytes : 0;
-  l.part_bytes = l.splits > 1 ? tiles * l.splits * (mt / 16) * 64 * 16 : 0;
   return l;
 }
 static_assert(kSplitkCounterBytes % 256 == 0, "partials stay 256-byte aligned");
@@ -730,8 +1112,12 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
   p.K = K;
   p.group_size = group_size;
   p.groups = K / group_size;
+  // The GEMM has no RMSNorm prologue; its epilogue reads bias four at a time
+  // and its loads take whole 4-byte words of the zero-point table.
+  const bool use_gemm = M > kGemmMinRows && !norm_weight && K % gemm::BK == 0 && (!bias || aligned(bias, 8)) &&
+                        aligned(zeros, 4);
   int splits = 1;
-  if (splitk) {
+  if (splitk && (use_gemm || M <= kGemmMinRows)) {
     const SplitkLayout l = splitk_layout(M, N, K);
     if (l.splits > 1) {
       if (!workspace || !aligned(workspace, 256) ||
@@ -744,8 +1130,13 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
     }
   }
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  const hipError_t e =
-      dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s, splits) : launch_int4_linear<BF16>(p, s, splits);
+  hipError_t e;
+  if (use_gemm) {
+    GemmShape gs = gemm_shape(M, N, K, splits > 1);
+    gs.splits = splits;
+    e = dtype == NS_DTYPE_F16 ? launch_int4_gemm<F16>(p, gs, s) : launch_int4_gemm<BF16>(p, gs, s);
+  } else
+    e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s, splits) : launch_int4_linear<BF16>(p, s, splits);
   return e == hipSuccess ? NS_OK : NS_ERR_HIP;
 }
 

@@ -9,8 +9,10 @@ so checkpoints quantised either way are interchangeable.
 
 The difference is the forward.  The reference's QuantLinear expands the whole
 weight to fp16 on every call and then runs F.linear (quant.py:149-158); here
-`Int4Linear.forward` calls `ns_int4_linear`, which dequantises each weight in
-registers on its way into the MFMA and never writes the expanded weight.
+`Int4Linear.forward` calls `ns_int4_linear`, which never writes the expanded
+weight: up to FUSED_MAX_ROWS rows it dequantises each weight in registers on
+its way into the MFMA, above that (prefill chunks) a tiled GEMM dequantises
+each 128 x 64 weight tile once into LDS and shares it with 128 tokens.
 """
 
 from __future__ import annotations
@@ -21,11 +23,11 @@ import torch.nn.functional as F
 
 from . import _lib
 
-# Up to this many rows ns_int4_linear dequantises inside its MFMA tiles; above
-# it, one dequantisation pass plus a library GEMM is faster (each 64-row tile
-# of the fused kernel repeats the dequantisation of its weight tile).  MI355X,
-# Qwen2.5-0.5B shapes: the two are even at 128 rows; at 2048 rows gate|up
-# takes 94 us this way against 422 us fused.
+# Up to this many rows ns_int4_linear dequantises inside its MFMA tiles (and
+# can fuse the input RMSNorm and the rotary + cache-write epilogue); above it
+# the library runs its tiled GEMM, which shares each dequantised weight tile
+# among 128 tokens (each 64-row tile of the register path would repeat the
+# dequantisation of its weight tile).
 FUSED_MAX_ROWS = 128
 
 # Dequantised-weight scratch per (device, stream), grown on demand.
@@ -86,9 +88,18 @@ def quantize_int4_groupwise(w: torch.Tensor, group_size: int = 128):
 
 @torch.inference_mode()
 def splitk_workspace_bytes(N: int, K: int) -> int:
-    """Workspace bytes that cover every fused-path token count (1..FUSED_MAX_ROWS) of an N x K layer."""
+    """Workspace bytes that cover every token count of an N x K layer.
+
+    The fused kernel (1..FUSED_MAX_ROWS rows) and the tiled GEMM (above) only
+    split K while their tiles are few; the GEMM's partials depend on M through
+    its count of 64- or 128-row tiles of 64 features, and it stops splitting
+    once ceil(M/128) * ceil(N/64) exceeds 256, so the scan below (every
+    multiple of 64 rows) ends there.
+    """
     lib = _lib.load()
-    return max(int(lib.ns_int4_linear_splitk_workspace_size(m, N, K)) for m in range(1, FUSED_MAX_ROWS + 1))
+    rows = list(range(1, FUSED_MAX_ROWS + 1))
+    rows += [64 * j for j in range(3, 2 * (256 // -(-N // 64)) + 3)]
+    return max(int(lib.ns_int4_linear_splitk_workspace_size(m, N, K)) for m in rows)
 
 
 def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
@@ -103,10 +114,13 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
     be a multiple of 128 and at most 1024).
     workspace: a zeroed uint8 buffer of splitk_workspace_bytes(N, K) bytes;
     given, long-K layers split their K loop over several workgroups per tile
-    (ns_int4_linear_splitk).  Calls that overlap in time must not share one.
-    method: "fused" (ns_int4_linear), "dequant" (ns_int4_dequantize, then a
-    library GEMM and the same epilogue as tensor ops) or "auto" (fused up to
-    FUSED_MAX_ROWS rows).
+    when their tiles alone would leave CUs idle (ns_int4_linear_splitk, both
+    kernels).  Calls that overlap in time must not share one.
+    method: "fused" or "auto" (ns_int4_linear: the register-dequant kernel up
+    to FUSED_MAX_ROWS rows, the tiled GEMM above; above FUSED_MAX_ROWS the
+    RMSNorm runs first as its own op) or "dequant" (ns_int4_dequantize, then
+    a library GEMM and the same epilogue as tensor ops: the reference's
+    QuantLinear steps, kept for comparison).
     residual: [..., N] added to the result in the same launch (the reference's
     `residual + o_proj(x)`, rounded as two tensor ops).  silu_mul: the weight's
     rows are interleaved (gate, up) pairs and the result is
@@ -149,7 +163,7 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
         raise ValueError(f"out must be a contiguous [{M}, {n_out}] {x.dtype} tensor")
     if method not in ("auto", "fused", "dequant"):
         raise ValueError(f"unknown method {method!r}")
-    if method == "dequant" or (method == "auto" and M > FUSED_MAX_ROWS):
+    if method == "dequant":
         w = _scratch_weight(x.device, N, K, x.dtype)
         int4_dequantize(qweight, scales, zeros, group_size, x.dtype, out=w)
         xin = x2 if norm_weight is None else F.rms_norm(x2, (K,), norm_weight, norm_eps)
@@ -164,7 +178,12 @@ def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, ze
     if norm_weight is not None:
         if norm_weight.shape != (K,) or norm_weight.dtype != x.dtype or not norm_weight.is_contiguous():
             raise ValueError(f"norm_weight must be a contiguous [{K}] {x.dtype} tensor")
-        nw_ptr = norm_weight.data_ptr()
+        if M > FUSED_MAX_ROWS:
+            # The tiled GEMM has no RMSNorm prologue: normalise as its own op
+            # (the reference's separate RMSNorm, torch's fused kernel).
+            x2 = F.rms_norm(x2, (K,), norm_weight, norm_eps).contiguous()
+        else:
+            nw_ptr = norm_weight.data_ptr()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     if workspace is not None:
         if workspace.dtype != torch.uint8 or not workspace.is_cuda or workspace.data_ptr() % 256 != 0:

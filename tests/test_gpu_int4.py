@@ -23,8 +23,8 @@ RTOL = {torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}
 NAME = {torch.float16: "float16", torch.bfloat16: "bfloat16"}
 
 # Qwen2.5-0.5B projections (in -> out): q, k/v, o, gate/up, down, and fused q|k|v, gate|up.
-# Arrival-counter region at the head of every split-K workspace (128 tiles x u32).
-SPLITK_COUNTER_BYTES = 512
+# Arrival-counter region at the head of every split-K workspace (256 tiles x u32).
+SPLITK_COUNTER_BYTES = 1024
 
 QWEN = [(896, 896), (896, 128), (896, 4864), (4864, 896), (896, 1152), (896, 9728)]
 
@@ -138,9 +138,11 @@ def _round(a: np.ndarray, dtype) -> np.ndarray:
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("K,N,M", [(896, 896, 32), (4864, 896, 32), (4864, 896, 5), (896, 1152, 100)])
+@pytest.mark.parametrize("K,N,M", [(896, 896, 32), (4864, 896, 32), (4864, 896, 5), (896, 1152, 100),
+                                   (896, 896, 300), (4864, 896, 1030)])
 def test_residual_epilogue(dtype, K, N, M):
-    """out = round(round(x W^T + b) + residual), also in place on the residual."""
+    """out = round(round(x W^T + b) + residual), also in place on the residual
+    (M of 300 and 1030: the tiled GEMM's epilogue)."""
     packed, s, z = _weights(N, K, 128, 11)
     g = torch.Generator().manual_seed(12)
     x = torch.randn(M, K, generator=g).to(dtype)
@@ -162,9 +164,11 @@ def test_residual_epilogue(dtype, K, N, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M", [1, 32, 70])
+@pytest.mark.parametrize("M", [1, 32, 70, 300, 1100])
 def test_silu_mul_epilogue_on_interleaved_gate_up(dtype, M):
-    """Interleaved (gate, up) rows -> round(round(silu(round(g))) * round(u)), [M, N/2]."""
+    """Interleaved (gate, up) rows -> round(round(silu(round(g))) * round(u)), [M, N/2]
+    (M = 300: the tiled GEMM's epilogue on 64 x 64 tiles; 1100: on 128 x 128 tiles,
+    the last one partly past M)."""
     from nanoserve_amd.quant import Int4Linear
 
     K, I = 896, 4864
@@ -243,9 +247,22 @@ def test_dequantize_is_bit_exact(dtype, N, K, gs):
 
 
 @pytest.mark.parametrize("M", [129, 700, 2048])
-def test_large_row_counts_take_the_dequant_path_within_one_rounding(M):
+def test_large_row_counts_take_the_tiled_gemm_within_one_rounding(M):
+    """Every tile shape of the GEMM: 64 x 64 (all but the cases below), 128 tokens
+    x 64 features (K = 4864 at 2048 tokens), 128 x 128 (N = 4096 at 2048 tokens)."""
     _run(M, 1152, 896, torch.float16, seed=M)
     _run(M, 896, 4864, torch.bfloat16, seed=M + 1)
+    _run(M, 4096, 512, torch.bfloat16, seed=M + 2)
+
+
+@pytest.mark.parametrize("gs", [32, 64, 256])
+@pytest.mark.parametrize("M,N", [(130, 2048), (513, 1152)])
+def test_tiled_gemm_group_sizes_and_partial_tiles(gs, M, N):
+    """Token tiles past M (rows repeat the last one and are never stored), feature
+    tiles past N (N = 1152 is nine 128-row tiles; 2048 sixteen), and group sizes
+    below and above the 64-wide K step."""
+    _run(M, N, 768, torch.float16, gs=gs, seed=M + gs)
+    _run(M, N, 512, torch.bfloat16, gs=gs, bias=False, seed=M + gs + 1)
 
 
 @pytest.mark.parametrize("method", ["fused", "dequant"])
@@ -360,11 +377,12 @@ def test_rope_cache_epilogue_matches_projection_then_rotary(dtype, M, heads, wit
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("M", [1, 16, 33, 64, 100])
+@pytest.mark.parametrize("M", [1, 16, 33, 64, 100, 200, 700, 2048])
 def test_splitk_down_projection(dtype, M):
     """ns_int4_linear_splitk on down_proj's shape (N 896, K 4864; 4 splits per
     16-token tile up to 16 tokens, 2 up to 32, none at 33-64; beyond 64 tokens the
-    tiles are 64 tokens wide and split twice again): within one rounding of the oracle on
+    tiles are 64 tokens wide and split twice again; above 128 tokens the tiled GEMM
+    splits its 128 x 64 tiles 4 times up to 1152 tokens, then 3 and 2): within one rounding of the oracle on
     the residual epilogue, identical on a repeated call (the arrival counters are back
     at zero), identical rows for a batch and its first row alone when both split the
     same way, and within one rounding of the unsplit kernel."""
@@ -403,7 +421,8 @@ def test_splitk_workspace_reused_across_token_counts(dtype):
     call to call, as a layer's decode steps do (M = 1, 32, 100, 1, 17, 8): each call
     equals, bit for bit, the same call on a fresh zeroed workspace, and the whole
     arrival-counter region is back at zero after every call.  A small-M call's
-    partial sums must never land where a larger-M call keeps its counters."""
+    partial sums must never land where a larger-M call keeps its counters (the
+    300- and 1500-token calls split in the tiled GEMM, the rest in the fused kernel)."""
     from nanoserve_amd.quant import splitk_workspace_bytes
 
     N, K = 896, 4864
@@ -412,7 +431,7 @@ def test_splitk_workspace_reused_across_token_counts(dtype):
     shared = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
     g = torch.Generator().manual_seed(82)
     b = (torch.randn(N, generator=g) * 0.1).to(dtype).to(DEV)
-    for M in (1, 32, 100, 1, 17, 8, 32):
+    for M in (1, 32, 300, 100, 1, 1500, 17, 8, 32):
         print(f"splitk reuse M={M} {dtype}", flush=True)
         x = torch.randn(M, K, generator=g).to(dtype).to(DEV)
         res = torch.randn(M, N, generator=g).to(dtype).to(DEV)
