@@ -45,6 +45,7 @@ import time
 
 METRIC = "paged-attn decode HBM GB/s (% of peak) + µs/call, B=32 Qwen-0.5B heads"
 HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
 
 WORKLOADS = {
     "c1": "decode B=8 ctx U[64,512] Hq14/Hkv2/D64 block16 fp16, 256-block pool",
@@ -81,6 +82,9 @@ def parse_args(argv=None):
                     help="only time an empty launch and streaming reads of c2's byte counts and exit")
     ap.add_argument("--ref-grid", action="store_true",
                     help="only run the reference's B x uniform-ctx grid (with its correctness gate) and exit")
+    ap.add_argument("--int4-gemm", action="store_true",
+                    help="only time ns_int4_linear on the Qwen2.5-0.5B projections at prefill sizes "
+                         "(and the reference's dequantise + library GEMM steps beside it) and exit")
     ap.add_argument("--copy-calibration", type=float, default=None, metavar="MB",
                     help="only run 5 plain device copies of MB megabytes (the known-size kernel that "
                          "scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings) and exit")
@@ -196,6 +200,44 @@ def _graph_time(torch, stream, launch, n, reps=3):
             end.synchronize()
             best = min(best, start.elapsed_time(end) * 1e-3 / n)
     return best
+
+
+def _int4_gemm(torch, args):
+    """ns_int4_linear at prefill token counts on the Qwen2.5-0.5B projections
+    (fp16 activations, INT4 g128 weights, each projection with the epilogue the
+    model gives it), graph-replayed, against the reference's QuantLinear steps
+    (dequantize_int4 then F.linear, then the epilogue as tensor ops) on the same
+    operands.  Down_proj runs with its split-K workspace, as Int4Linear does."""
+    from nanoserve_amd.quant import int4_linear, quantize_int4_groupwise, splitk_workspace_bytes
+
+    stream = torch.cuda.Stream()
+    gen = torch.Generator().manual_seed(args.seed)
+    rows = []
+    for name, K, N, epi in (("qkv", 896, 1152, "bias"), ("o_proj", 896, 896, "residual"),
+                            ("gate_up", 896, 9728, "silu_mul"), ("down_proj", 4864, 896, "residual")):
+        packed, scales, zeros = (t.to("cuda") for t in
+                                 quantize_int4_groupwise(torch.randn(N, K, generator=gen) * 0.05, 128))
+        ws = torch.zeros(max(splitk_workspace_bytes(N, K), 256), dtype=torch.uint8, device="cuda")
+        for M in (256, 1024, 2048):
+            x = torch.randn(M, K, generator=gen).half().to("cuda")
+            bias = (torch.randn(N, generator=gen) * 0.1).half().to("cuda") if epi == "bias" else None
+            res = torch.randn(M, N, generator=gen).half().to("cuda") if epi == "residual" else None
+            t = {}
+            for method in ("fused", "dequant"):
+                def launch(i, method=method):
+                    int4_linear(x, packed, scales, zeros, bias, 128, residual=res, silu_mul=epi == "silu_mul",
+                                method=method, workspace=ws if method == "fused" else None)
+                t[method] = _graph_time(torch, stream, launch, 20)
+            flops = 2 * M * N * K
+            rows.append({"proj": name, "tokens": M, "N": N, "K": K, "epilogue": epi,
+                         "us": round(t["fused"] * 1e6, 2), "tflops": round(flops / t["fused"] / 1e12, 1),
+                         "frac_of_mfma_peak": round(flops / t["fused"] / 1e12 / MFMA_PEAK_TFLOPS, 4),
+                         "reference_steps_us": round(t["dequant"] * 1e6, 2)})
+    print(json.dumps({"int4_gemm": rows, "device": torch.cuda.get_device_name(0),
+                      "timing": "HIP-graph replay of 20 back-to-back calls, hipEvents, best of 3",
+                      "mfma_peak_tflops": MFMA_PEAK_TFLOPS,
+                      "reference_steps": "ns_int4_dequantize + torch F.linear (hipBLASLt) + epilogue ops"}))
+    return 0
 
 
 def _floors(torch, args):
@@ -640,6 +682,8 @@ def main(argv=None):
         return _copy_calibration(torch, args.copy_calibration)
     if args.floors:
         return _floors(torch, args)
+    if args.int4_gemm:
+        return _int4_gemm(torch, args)
     if args.ref_grid:
         return _ref_grid(torch, args)
     if args.config == "c5":
