@@ -818,6 +818,9 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
 // --------------------------------------------------------------------------
 template <int D, int CT_>
 struct PrefillCfg {
+  // Four key groups of two column waves (32 keys a step, 64 columns per
+  // workgroup) measured slower at c3 than two groups of four (51.0 against
+  // 45.2 us per call): twice the workgroups, still one per CU.
   static constexpr int KG = 2;                  // key groups
   static constexpr int WC = 4;                  // column waves per group
   static constexpr int W = KG * WC;             // waves per workgroup
@@ -827,7 +830,7 @@ struct PrefillCfg {
   static constexpr int NT = KT / 16, NC = D / 32, NN = D / 16;
   static constexpr int CPR = D / 8;             // 16-byte chunks per key row
   static constexpr int TILE = KT * D * 2;       // bytes of one K or V tile
-  static constexpr int DMA = TILE / (THREADS * 16);  // 16-byte loads per thread per tile
+  static constexpr int DMA = KG * TILE / (THREADS * 16);  // 16-byte loads per thread per K (or V) of a macro-step
   static constexpr int NSLOT = 3;               // macro-slots in the ring
   static constexpr int RING = NSLOT * KG * 2 * TILE;
   static constexpr int TBL = 4096;              // table entries per window
@@ -836,7 +839,7 @@ struct PrefillCfg {
   static constexpr int NF = CT * (NN * 4 + 2);  // floats per lane a group hands over in the merge
   static constexpr int PU = CT * (NN + 1);      // 16-byte units per lane of a split's partial
   static constexpr int SLOT_BYTES = WC * PU * 64 * 16;
-  static_assert(DMA >= 1 && DMA * THREADS * 16 == TILE, "loads must tile a K/V tile");
+  static_assert(DMA >= 1 && DMA * THREADS * 16 == KG * TILE && TILE % 1024 == 0, "loads must tile a macro-step");
   static_assert(NT % 2 == 0, "P^T operand pairs two 16-key tiles");
   static_assert(WC * NF * 64 * 4 <= RING, "merge buffer fits the ring");
 };
@@ -979,25 +982,30 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
   int e0 = 0;      // first table entry of the current window
   int kv_win = 0;  // keys covered by the window's entries (and below kv_end)
 
-  // Start the K/V loads of `step` into `stage`.  Lane `lane` of load u of
-  // wave w fills 16-byte slot (u * W + w) * 64 + lane of each tile.  Keys
-  // past the window or kv_end read an in-bounds slot; their scores are
-  // masked and their V values replaced by zero when read.
-  auto dma = [&](int step, int stage) {
-    char* st = smem + stage * 2 * TILE;
+  // Start the K/V loads of macro-step M into macro-slot `slot` (stages
+  // slot * KG + k, k < KG, one per step).  Load u of wave w covers the 1 KiB
+  // piece b = u * W + w of the macro-step's K (and of its V): piece b % PT of
+  // step M * KG + b / PT, lane `lane` filling its 16-byte slot b % PT * 64 +
+  // lane.  Keys past the window or kv_end read an in-bounds slot; their
+  // scores are masked and their V values replaced by zero when read.
+  auto dma_macro = [&](int M, int slot) {
+    constexpr int PT = TILE / 1024;  // 1 KiB pieces per tile
 #pragma unroll
     for (int u = 0; u < DMA; ++u) {
-      const int pos = (u * W + w) * 64 + lane;
+      const int b = u * W + w;
+      const int k = b / PT, piece = b % PT;
+      char* st = smem + (slot * KG + k) * 2 * TILE;
+      const int pos = piece * 64 + lane;
       const int key = pos / CPR, pc = pos % CPR;
-      const int t = step * KT + key;
+      const int t = (M * KG + k) * KT + key;
       const bool in = t < kv_win;
       const int blk = tbl[in ? (t >> bs_shift) - e0 : 0];
       const bool valid = in && blk >= 0;
       const int64_t off = valid ? ((static_cast<int64_t>(blk) << bs_shift) + (t & bs_mask)) * slot_stride : 0;
       const T* gk = kbase + off + ((pc ^ k_swz(key)) << 3);
       const T* gv = vbase + off + ((pc ^ v_swz(key)) << 3);
-      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gk), (lds_void_ptr)(st + (u * W + w) * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gv), (lds_void_ptr)(st + TILE + (u * W + w) * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gk), (lds_void_ptr)(st + piece * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void_ptr)(gv), (lds_void_ptr)(st + TILE + piece * 1024), 16, 0, 0);
     }
   };
 
@@ -1022,12 +1030,30 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
         for (int c2 = 0; c2 < NC; ++c2) sacc[ct][j] = mfma16x16x32(DT{}, kop[c2], qop[ct][c2], sacc[ct][j]);
       }
     }
+    // The V^T operands of the whole step (see the PV product below), issued
+    // now as asm so their LDS latency hides behind the softmax.  Through the
+    // builtin, the compiler's wait-count pass would put an s_waitcnt vmcnt(0)
+    // in front of the first one (it cannot tell them from the K/V loads in
+    // flight into the ring), draining the prefetch of the next macro-steps.
+    const int d0 = 4 * (c16 & 3);
+    u32x2 vraw[NT / 2][NN][2];
+#pragma unroll
+    for (int pb = 0; pb < NT / 2; ++pb)
+#pragma unroll
+      for (int n = 0; n < NN; ++n)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int key = 32 * pb + 16 * h + 4 * g + (c16 >> 2);
+          const int d = 16 * n + d0;
+          vraw[pb][n][h] = ds_read_tr16_b64(vt + key * D * 2 + (((d >> 3) ^ v_swz(key)) << 4) + ((d & 7) << 1));
+        }
     // Online softmax in base 2 (sc = |scale| * log2 e).  When every key of the
     // step precedes every column of the wave, the maximum is taken over raw
     // scores and p = exp2(s * sc - m) is one FMA; otherwise key
     // tb + 16j + 4g + r of a column is masked by the column's limit.
     const bool full = tb + KT - 1 <= qmin_w;
-    V8 pt[CT][NT / 2];
+    const bool vfull = tb + KT <= kv_end;
+    V8 pt[CT][NT / 2], va[NT / 2][NN];
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       float sv[NT][4];
@@ -1082,40 +1108,38 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
           pt[ct][pb][e] = static_cast<T>(sv[2 * pb][e]);
           pt[ct][pb][4 + e] = static_cast<T>(sv[2 * pb + 1][e]);
         }
-    }
-    // O^T += V^T P^T.  k-slot 4h + e of lane group g is key 32pb + 16h + 4g + e,
-    // matching P^T.  ds_read_b64_tr_b16 gives lane i of a 16-lane group
-    // element e = element i & 3 of the 8 bytes lane (i >> 2) + 4e of the group
-    // addressed, so lane c16 of group g points at head dims 16n + 4 (c16 & 3)
-    // .. +3 of key 32pb + 16h + 4g + (c16 >> 2) and receives V^T row 16n + c16
-    // at keys 32pb + 16h + 4g + 0..3.  Keys at or past kv_end (only in the
-    // last step) contribute zero.
-    const bool vfull = tb + KT <= kv_end;
-    const int d0 = 4 * (c16 & 3);
+      // O^T += V^T P^T for this column tile, right after its softmax: the
+      // MFMAs run while the next tile's softmax issues.  k-slot 4h + e of lane
+      // group g is key 32pb + 16h + 4g + e, matching P^T.  ds_read_b64_tr_b16
+      // gives lane i of a 16-lane group element e = element i & 3 of the 8
+      // bytes lane (i >> 2) + 4e of the group addressed, so lane c16 of group
+      // g points at head dims 16n + 4 (c16 & 3) .. +3 of key 32pb + 16h + 4g +
+      // (c16 >> 2) and receives V^T row 16n + c16 at keys 32pb + 16h + 4g +
+      // 0..3.  Keys at or past kv_end (only in the last step) contribute zero.
+      if (ct == 0) {
+        lds_wait_all();
 #pragma unroll
-    for (int pb = 0; pb < NT / 2; ++pb)
+        for (int pb = 0; pb < NT / 2; ++pb)
 #pragma unroll
-      for (int n = 0; n < NN; ++n) {
-        u32x2 half_op[2];
+          for (int n = 0; n < NN; ++n) {
+            lds_ready(vraw[pb][n][0]);
+            lds_ready(vraw[pb][n][1]);
+            va[pb][n] = __builtin_bit_cast(
+                V8, u32x4{vraw[pb][n][0][0], vraw[pb][n][0][1], vraw[pb][n][1][0], vraw[pb][n][1][1]});
+            if (!vfull) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int key = 32 * pb + 16 * h + 4 * g + (c16 >> 2);
-          const int d = 16 * n + d0;
-          const char* src = vt + key * D * 2 + (((d >> 3) ^ v_swz(key)) << 4) + ((d & 7) << 1);
-          half_op[h] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                      (__attribute__((address_space(3))) short4_t*)(src)));
-        }
-        V8 va = __builtin_bit_cast(V8, u32x4{half_op[0][0], half_op[0][1], half_op[1][0], half_op[1][1]});
-        if (!vfull) {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const int key = 32 * pb + 16 * (e >> 2) + 4 * g + (e & 3);
-            va[e] = tb + key < kv_end ? va[e] : static_cast<T>(0.f);
+              for (int e = 0; e < 8; ++e) {
+                const int key = 32 * pb + 16 * (e >> 2) + 4 * g + (e & 3);
+                va[pb][n][e] = tb + key < kv_end ? va[pb][n][e] : static_cast<T>(0.f);
+              }
+            }
           }
-        }
-#pragma unroll
-        for (int ct = 0; ct < CT; ++ct) acc[ct][n] = mfma16x16x32(DT{}, va, pt[ct][pb], acc[ct][n]);
       }
+#pragma unroll
+      for (int pb = 0; pb < NT / 2; ++pb)
+#pragma unroll
+        for (int n = 0; n < NN; ++n) acc[ct][n] = mfma16x16x32(DT{}, va[pb][n], pt[ct][pb], acc[ct][n]);
+    }
   };
 
   if (tid == 0) *bad_first = 0x7FFFFFFF;
@@ -1131,10 +1155,6 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     M_end = M_begin + split_mk < nmacro ? M_begin + split_mk : nmacro;
   }
   const int win_macro = (Cfg::TBL << bs_shift) / MKEYS;
-  auto dma_macro = [&](int M, int slot) {
-#pragma unroll
-    for (int k = 0; k < KG; ++k) dma(M * KG + k, slot * KG + k);
-  };
   for (int M0 = M_begin; M0 < M_end; M0 += win_macro) {
     const int M1 = M0 + win_macro < M_end ? M0 + win_macro : M_end;
     e0 = (M0 * MKEYS) >> bs_shift;
@@ -1163,7 +1183,7 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     __syncthreads();
 
     // Macro-steps M0 .. M1-1 through the three slots: at the top of macro-step
-    // M the loads of M+1 may still be in flight (KG * 2 * DMA per thread), M's
+    // M the loads of M+1 may still be in flight (2 * DMA per thread), M's
     // have landed once every wave has waited for its own and passed the
     // barrier; then M+2's loads go into the slot M-1 used.  Macro-steps past
     // M1 still load (nothing valid) so the pending count stays exact.
@@ -1171,7 +1191,7 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     dma_macro(M0 + 1, 1);
     int slot = 0;
     for (int M = M0; M < M1; ++M) {
-      stage_barrier<KG * 2 * DMA>();
+      stage_barrier<2 * DMA>();
       dma_macro(M + 2, slot == 0 ? 2 : slot - 1);
       compute(slot * KG + kg, M * KG + kg);
       slot = slot == 2 ? 0 : slot + 1;
