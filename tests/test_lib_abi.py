@@ -198,6 +198,23 @@ def test_int4_linear_splitk_checks_its_workspace():
         _lib.NS_ERR_INVALID_ARG
 
 
+@pytest.mark.parametrize("N,K", [(896, 4864), (896, 896), (1152, 896), (9728, 896), (4096, 8192)])
+def test_splitk_workspace_bytes_cover_every_token_count(N, K):
+    """The module-level workspace (sized once per layer by a scan of token counts)
+    is at least what the library asks for at every M, through the register
+    kernel's range and the tiled GEMM's, past the point where neither splits;
+    the GEMM splits down_proj at prefill sizes (a non-zero size above 128 rows)."""
+    from nanoserve_amd.quant import splitk_workspace_bytes
+
+    lib = _lib.load()
+    have = splitk_workspace_bytes(N, K)
+    sizes = [lib.ns_int4_linear_splitk_workspace_size(m, N, K) for m in range(1, 6000)]
+    assert max(sizes) <= have
+    if (N, K) == (896, 4864):
+        assert lib.ns_int4_linear_splitk_workspace_size(1024, N, K) > 0
+        assert lib.ns_int4_linear_splitk_workspace_size(2048, N, K) > 0
+
+
 def test_int4_linear_rope_cache_rejects_bad_arguments():
     lib = _lib.load()
 
