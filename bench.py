@@ -207,7 +207,7 @@ def _int4_gemm(torch, args):
     (fp16 activations, INT4 g128 weights, each projection with the epilogue the
     model gives it), graph-replayed, against the reference's QuantLinear steps
     (dequantize_int4 then F.linear, then the epilogue as tensor ops) on the same
-    operands.  Down_proj runs with its split-K workspace, as Int4Linear does."""
+    operands.  Every projection runs with a split-K workspace, as Int4Linear does."""
     from nanoserve_amd.quant import int4_linear, quantize_int4_groupwise, splitk_workspace_bytes
 
     stream = torch.cuda.Stream()

@@ -166,8 +166,12 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
  * as ns_int4_linear; the fp32 partial sums of each split go to `workspace`
  * and the last split of a tile adds them in split order (deterministic) and
  * runs the epilogue.  The split count (up to 4) keeps tiles x splits within
- * 256 workgroups up to 128 tokens (register-dequant kernel) and within 512
- * above (tiled GEMM), so it depends on N, K and the number of token tiles.
+ * 256 workgroups up to 128 tokens (register-dequant kernel); above (tiled
+ * GEMM), the tiles of the last dispatch round split (all tiles when one round
+ * holds them) when they fill at most half of the device's slots, within
+ * those slots and with at least 8 K steps of 64 a split, so it depends on N,
+ * K and the number of token tiles, and the partials never exceed one round
+ * of fp32 tiles (32 MiB).
  * Same replacement as ns_int4_linear (reference
  * nanoserve/quant.py:157-158).  workspace: 256-byte aligned,
  * ns_int4_linear_splitk_workspace_size(M, N, K) bytes, zeroed once before

@@ -65,6 +65,11 @@ struct Int4LinearParams {
   float* part;
   unsigned* counters;
   int part_bytes;
+  // Tiled GEMM (1-D grid): gemm_gx feature tiles per token tile; tiles
+  // 0 .. gemm_whole-1 run whole, one workgroup each, and every later tile as
+  // gemm_splits K splits (split-K for the tiles of a last, part-filled
+  // dispatch round, or for every tile when gemm_whole is 0).
+  int gemm_gx, gemm_whole, gemm_splits;
 };
 
 // Device-scope (sc1) buffer accesses carry partials between workgroups, which
@@ -715,10 +720,12 @@ bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q)
 // (the loads are issued from asm, invisible to the compiler's wait-count
 // pass).
 //
-// Split-K (gridDim.z = S > 1, long-K layers with few tiles): split z walks
-// steps [z*steps/S, (z+1)*steps/S), publishes its fp32 partial tile to the
+// Split-K (tiles past gemm_whole, S = gemm_splits > 1): split z walks steps
+// [z*steps/S, (z+1)*steps/S), publishes its fp32 partial tile to the
 // workspace and counts its arrival; the last split of the tile adds all S
-// partials in split order and applies the epilogue.
+// partials in split order and applies the epilogue.  The split tiles come
+// last in the grid, so when the whole tiles fill the device for some rounds
+// the splits share out the last round's tiles over its otherwise idle slots.
 // --------------------------------------------------------------------------
 constexpr int64_t kGemmMinRows = 128;  // the fused kernel takes M up to here
 namespace gemm {
@@ -775,12 +782,22 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = w % WN, wm = w / WN;
-  // Grid: feature tiles along x (consecutive workgroups share one x row
-  // block, spread over the XCDs by the round-robin dispatch: an XCD-local
-  // renumbering measured slower), token tiles along y, K splits along z.
-  const int gx = gridDim.x, S = gridDim.z, z = blockIdx.z;
-  const int tile = blockIdx.y * gx + blockIdx.x;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  // Grid: tile t = (token tile t / gx, feature tile t % gx), so consecutive
+  // workgroups share one x row block, spread over the XCDs by the round-robin
+  // dispatch (an XCD-local renumbering measured slower).  Workgroup b <
+  // gemm_whole takes tile b whole; the rest take split z of tile gemm_whole +
+  // st, workgroup gemm_whole + z * split_tiles + st, so one round of splits
+  // covers every split tile.
+  const int gx = p.gemm_gx, b = blockIdx.x;
+  const int split_tiles = ((p.M + BM - 1) / BM) * gx - p.gemm_whole;
+  int S = 1, z = 0, st = 0, tile = b;
+  if (b >= p.gemm_whole) {
+    S = p.gemm_splits;
+    st = (b - p.gemm_whole) % split_tiles;
+    z = (b - p.gemm_whole) / split_tiles;
+    tile = p.gemm_whole + st;
+  }
+  const int n0 = (tile % gx) * BN, m0 = (tile / gx) * BM;
   const int steps = p.K / BK;
   const int s0 = z * steps / S, s1 = (z + 1) * steps / S;
 
@@ -895,7 +912,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
     __shared__ unsigned last_arrival;
     const __amdgpu_buffer_rsrc_t rs =
         __builtin_amdgcn_make_buffer_rsrc(p.part, static_cast<short>(0), p.part_bytes, kBufferWord3);
-    auto off = [&](int zz, int fi, int ti) { return ((((tile * S + zz) * WAVES + w) * FT + fi) * TT + ti) * 1024 + lane * 16; };
+    auto off = [&](int zz, int fi, int ti) { return ((((st * S + zz) * WAVES + w) * FT + fi) * TT + ti) * 1024 + lane * 16; };
 #pragma unroll
     for (int fi = 0; fi < FT; ++fi)
 #pragma unroll
@@ -904,7 +921,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partial stores are acknowledged
     __syncthreads();                     // ... by every wave
     if (tid == 0)
-      last_arrival = __hip_atomic_fetch_add(&p.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+      last_arrival = __hip_atomic_fetch_add(&p.counters[st], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                      static_cast<unsigned>(S - 1);
     __syncthreads();
     if (!last_arrival) return;
@@ -917,7 +934,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
           sum += __builtin_bit_cast(floatx4, __builtin_amdgcn_raw_buffer_load_b128(rs, off(zz, fi, ti), 0, kSc1));
         acc[fi][ti] = sum;
       }
-    if (tid == 0) __hip_atomic_store(&p.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&p.counters[st], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // D[4g + r][c16] of tile (fi, ti): features nf .. nf+3 of token m, rounded
@@ -967,37 +984,56 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
 }
 
 struct GemmShape {
-  int bm, bn, nst, wn, splits;
+  int bm, bn, nst, wn;
+  int64_t tiles, whole;  // all tiles; the first `whole` run unsplit
+  int splits;            // K splits of each later tile
 };
+
+// MI355X: 256 CUs of 160 KiB LDS; the kernels' LDS (not their registers)
+// sets how many workgroups share a CU.
+constexpr int kGemmCUs = 256;
+constexpr int kLdsPerCU = 160 * 1024;
+constexpr int gemm_lds(int bm, int bn, int nst) {
+  return nst * (bm * gemm::ROW_B + bn * gemm::BK / 2 + 2 * bn * 2 * 4) + 16;
+}
 
 // Tile shape and split count of a GEMM call, from measurements on MI355X
 // (fp16, Qwen2.5-0.5B projections, graph-replayed).  128 x 128 tiles when
 // they still give two workgroups per CU (gate|up from 1024 tokens: 44.8 /
-// 66.3 us at 1024 / 2048 tokens against 46.9 / 86.7 with 64 x 128 tiles);
+// 66.3 us at 1024 / 2048 tokens against 46.9 / 86.7 with 64 x 128 tiles,
+// both unsplit);
 // 128-token x 64-feature tiles for long-K layers with enough of them
 // (down_proj at 2048 tokens, split twice: 49.1 us against 53.9 with 64 x 128
 // tiles); 64 x 64 tiles otherwise, the most workgroups for short calls (qkv /
 // o / down at 256 tokens: 10.4 / 10.8 / 21.6 us, against 13.8 / 14.8 / 30.7
-// with 64 x 128).  Tiles that cannot fill the device split long K loops
-// (at least 8 steps a split) when the caller gave a workspace.
+// with 64 x 128).  When the caller gave a workspace and the tiles of the last
+// dispatch round (all of them, if one round holds every tile) fill at most
+// half of the device's slots, those tiles split their K loop, at least 8
+// steps a split: shorter splits write and read back more fp32 partials than
+// the idle slots win (gate|up at 1024 / 2048 tokens, its last round's 128 x
+// 128 tiles split into 4-5 steps: 49.4 / 74.9 us against 39.5 / 64.9 unsplit).
 GemmShape gemm_shape(int64_t M, int N, int K, bool can_split) {
   auto tiles = [&](int bm, int bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  GemmShape s{64, 64, 4, 4, 1};
-  if (tiles(128, 128) >= 512) s = {128, 128, 3, 4, 1};
-  else if (K >= 2048 && tiles(128, 64) >= 200) s = {128, 64, 3, 4, 1};
-  const int64_t t = tiles(s.bm, s.bn);
-  if (can_split && t * 2 <= 512 && t <= gemm::kMaxSplitTiles) {
+  GemmShape s{64, 64, 4, 4, 0, 0, 1};
+  if (tiles(128, 128) >= 512) s = {128, 128, 3, 4, 0, 0, 1};
+  else if (K >= 2048 && tiles(128, 64) >= 200) s = {128, 64, 3, 4, 0, 0, 1};
+  s.tiles = s.whole = tiles(s.bm, s.bn);
+  const int64_t slots = int64_t{kGemmCUs} * (kLdsPerCU / gemm_lds(s.bm, s.bn, s.nst));
+  const int64_t last = s.tiles - (s.tiles - 1) / slots * slots;  // tiles of the last round
+  if (can_split && 2 * last <= slots && last <= gemm::kMaxSplitTiles) {
     const int steps = K / gemm::BK;
-    s.splits = static_cast<int>(std::min<int64_t>(std::min(512 / t, int64_t{4}), steps / 8));
-    if (s.splits < 1) s.splits = 1;
+    const int64_t sp = std::min<int64_t>(std::min<int64_t>(slots / last, 4), steps / 8);
+    if (sp > 1) {
+      s.splits = static_cast<int>(sp);
+      s.whole = s.tiles - last;
+    }
   }
   return s;
 }
 
-int64_t gemm_part_bytes(int64_t M, int N, const GemmShape& s) {
+int64_t gemm_part_bytes(const GemmShape& s) {
   if (s.splits <= 1) return 0;
-  const int64_t tiles = ((M + s.bm - 1) / s.bm) * ((N + s.bn - 1) / s.bn);
-  return tiles * s.splits * static_cast<int64_t>(s.bm) * s.bn * 4;
+  return (s.tiles - s.whole) * s.splits * static_cast<int64_t>(s.bm) * s.bn * 4;
 }
 
 // Instantiated tile configurations: (BM, BN, NST, WN).
@@ -1016,9 +1052,9 @@ hipError_t launch_int4_gemm(const Int4LinearParams& p, const GemmShape& s, hipSt
   NS_INT4_GEMM_CONFIGS(NS_PICK)
 #undef NS_PICK
   if (!fn) return hipErrorInvalidValue;
-  const dim3 grid(static_cast<unsigned>((p.N + s.bn - 1) / s.bn), static_cast<unsigned>((p.M + s.bm - 1) / s.bm),
-                  static_cast<unsigned>(s.splits));
-  return hipLaunchKernel(fn, grid, dim3(gemm::THREADS), args, 0, stream);
+  const int64_t wgs = s.whole + (s.tiles - s.whole) * s.splits;
+  if (wgs > 0x7FFFFFFF) return hipErrorInvalidValue;
+  return hipLaunchKernel(fn, dim3(static_cast<unsigned>(wgs)), dim3(gemm::THREADS), args, 0, stream);
 }
 
 // Whole-weight dequantisation for large token counts, where a library GEMM on
@@ -1048,7 +1084,7 @@ namespace {
 // Split-K workspace: a fixed region of u32 arrival counters (one per tile,
 // zero between calls), then the partial sums.  The region has the same size
 // for every M: the fused kernel only splits when 2 * tiles <= 256 and the
-// GEMM when tiles <= gemm::kMaxSplitTiles, so at most 256 counters exist,
+// GEMM splits at most gemm::kMaxSplitTiles tiles, so at most 256 counters exist,
 // and the partials of any call start past every counter any other call may
 // use.  One workspace can therefore serve calls of every token count in turn
 // (a layer's decode steps change M from step to step) without a call's
@@ -1070,7 +1106,7 @@ SplitkLayout splitk_layout(int64_t M, int N, int K) {
     if (K % gemm::BK == 0) {
       const GemmShape gs = gemm_shape(M, N, K, true);
       l.splits = gs.splits;
-      l.part_bytes = gemm_part_bytes(M, N, gs);
+      l.part_bytes = gemm_part_bytes(gs);
     }
   } else {
     const int mt = M <= 64 ? 16 : 64;
@@ -1141,8 +1177,11 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
   const hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (use_gemm) {
-    GemmShape gs = gemm_shape(M, N, K, splits > 1);
-    gs.splits = splits;
+    // The same shape splitk_layout sized the workspace for (or none split).
+    const GemmShape gs = gemm_shape(M, N, K, splits > 1);
+    p.gemm_gx = (N + gs.bn - 1) / gs.bn;
+    p.gemm_whole = static_cast<int>(gs.whole);
+    p.gemm_splits = gs.splits;
     e = dtype == NS_DTYPE_F16 ? launch_int4_gemm<F16>(p, gs, s) : launch_int4_gemm<BF16>(p, gs, s);
   } else
     e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s, splits) : launch_int4_linear<BF16>(p, s, splits);

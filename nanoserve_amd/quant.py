@@ -12,7 +12,7 @@ weight to fp16 on every call and then runs F.linear (quant.py:149-158); here
 `Int4Linear.forward` calls `ns_int4_linear`, which never writes the expanded
 weight: up to FUSED_MAX_ROWS rows it dequantises each weight in registers on
 its way into the MFMA, above that (prefill chunks) a tiled GEMM dequantises
-each 128 x 64 weight tile once into LDS and shares it with 128 tokens.
+each weight tile once per 64- or 128-token tile.
 """
 
 from __future__ import annotations
@@ -86,20 +86,46 @@ def quantize_int4_groupwise(w: torch.Tensor, group_size: int = 128):
     return packed, scale.squeeze(2).contiguous(), zero.squeeze(2).to(torch.uint8).contiguous()
 
 
-@torch.inference_mode()
+# The tiled GEMM's split layout depends on M only through its tile shape
+# (chosen from ceil(M/128) and ceil(M/64)) and through how many tiles its
+# last dispatch round holds.  Every shape switch happens below 512 token
+# tiles of 128 rows, and past that the 128 x 128 tiles' last round repeats
+# every 512 token tiles (two workgroups per CU on 256 CUs), so multiples of
+# 64 rows up to twice that cover every token count.
+_SPLITK_SCAN_ROWS = 2 * 512 * 128
+
+
 def splitk_workspace_bytes(N: int, K: int) -> int:
     """Workspace bytes that cover every token count of an N x K layer.
 
-    The fused kernel (1..FUSED_MAX_ROWS rows) and the tiled GEMM (above) only
-    split K while their tiles are few; the GEMM's partials depend on M through
-    its count of 64- or 128-row tiles of 64 features, and it stops splitting
-    once ceil(M/128) * ceil(N/64) exceeds 256, so the scan below (every
-    multiple of 64 rows) ends there.
+    The fused kernel (1..FUSED_MAX_ROWS rows) splits K while its tiles are few;
+    the tiled GEMM (above) splits the tiles of a last dispatch round that
+    leaves at least half of the device idle, which can happen at any token
+    count, so the scan runs over every multiple of 64 rows up to the point
+    where the GEMM's layouts repeat.
     """
     lib = _lib.load()
     rows = list(range(1, FUSED_MAX_ROWS + 1))
-    rows += [64 * j for j in range(3, 2 * (256 // -(-N // 64)) + 3)]
+    rows += range(3 * 64, _SPLITK_SCAN_ROWS + 1, 64)
     return max(int(lib.ns_int4_linear_splitk_workspace_size(m, N, K)) for m in rows)
+
+
+# One split-K workspace per device serves every Int4Linear on it: their calls
+# run in stream order (the engine's eager steps and graph replays share one
+# stream) and a workspace's arrival counters are back at zero after each call,
+# so no call sees another's state.  A module keeps the buffer it was given; a
+# module that needs more than the current buffer gets a new, larger one, and
+# the old one stays with the modules (and captured graphs) that hold it.
+_splitk_shared: dict[int, torch.Tensor] = {}
+
+
+def _shared_splitk_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _splitk_shared.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _splitk_shared[key] = ws
+    return ws
 
 
 def int4_linear(x: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
@@ -292,8 +318,8 @@ class Int4Linear(nn.Module):
         # rotary-pair order (rope_pairs); forward() then restores row order.
         self.rope_heads: tuple[int, int, int] | None = None
         self.rope_inverse: torch.Tensor | None = None
-        # Split-K workspace of long-K layers (allocated zeroed on first use; one
-        # module's calls run in stream order, so they never overlap).
+        # Split-K workspace (taken on first use from the device's shared one;
+        # the INT4 layers' calls run in stream order, so they never overlap).
         self._splitk_ws: torch.Tensor | None = None
         self._splitk_checked = False
 
@@ -319,12 +345,12 @@ class Int4Linear(nn.Module):
         if not self._splitk_checked:
             n = splitk_workspace_bytes(self.out_features, self.in_features)
             if n and torch.cuda.is_current_stream_capturing():
-                # The zero fill would be recorded into the graph (and rerun by
-                # every replay); the first call belongs before capture.
+                # A new workspace's zero fill would be recorded into the graph
+                # (and rerun by every replay); the first call belongs before capture.
                 raise RuntimeError(
-                    f"Int4Linear({self.in_features}, {self.out_features}) allocates its split-K workspace "
+                    f"Int4Linear({self.in_features}, {self.out_features}) takes its split-K workspace "
                     "on first use: call it once before graph capture")
-            self._splitk_ws = torch.zeros(n, dtype=torch.uint8, device=self.qweight.device) if n else None
+            self._splitk_ws = _shared_splitk_workspace(self.qweight.device, n) if n else None
             self._splitk_checked = True
         y = int4_linear(x, self.qweight, self.scales, self.zeros,
                         None if self.bias is None else self.bias.data, self.group_size,

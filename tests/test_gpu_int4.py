@@ -382,7 +382,8 @@ def test_splitk_down_projection(dtype, M):
     """ns_int4_linear_splitk on down_proj's shape (N 896, K 4864; 4 splits per
     16-token tile up to 16 tokens, 2 up to 32, none at 33-64; beyond 64 tokens the
     tiles are 64 tokens wide and split twice again; above 128 tokens the tiled GEMM
-    splits its 128 x 64 tiles 4 times up to 1152 tokens, then 3 and 2): within one rounding of the oracle on
+    splits its 64 x 64 tiles 4 times up to 896 tokens and 3 times up to 1152, and
+    from 1793 tokens its 128 x 64 tiles twice): within one rounding of the oracle on
     the residual epilogue, identical on a repeated call (the arrival counters are back
     at zero), identical rows for a batch and its first row alone when both split the
     same way, and within one rounding of the unsplit kernel."""
@@ -422,7 +423,9 @@ def test_splitk_workspace_reused_across_token_counts(dtype):
     equals, bit for bit, the same call on a fresh zeroed workspace, and the whole
     arrival-counter region is back at zero after every call.  A small-M call's
     partial sums must never land where a larger-M call keeps its counters (the
-    300- and 1500-token calls split in the tiled GEMM, the rest in the fused kernel)."""
+    300-token call splits every tile of the tiled GEMM, the 4700-token call the
+    tiles of its last dispatch round, the 1500-token call none; the rest split
+    in the fused kernel)."""
     from nanoserve_amd.quant import splitk_workspace_bytes
 
     N, K = 896, 4864
@@ -431,7 +434,7 @@ def test_splitk_workspace_reused_across_token_counts(dtype):
     shared = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
     g = torch.Generator().manual_seed(82)
     b = (torch.randn(N, generator=g) * 0.1).to(dtype).to(DEV)
-    for M in (1, 32, 300, 100, 1, 1500, 17, 8, 32):
+    for M in (1, 32, 300, 100, 1, 1500, 4700, 17, 8, 32):
         print(f"splitk reuse M={M} {dtype}", flush=True)
         x = torch.randn(M, K, generator=g).to(dtype).to(DEV)
         res = torch.randn(M, N, generator=g).to(dtype).to(DEV)
@@ -442,3 +445,60 @@ def test_splitk_workspace_reused_across_token_counts(dtype):
         assert torch.equal(got, want), f"M={M}: reused workspace differs from a fresh one"
         assert not shared[:SPLITK_COUNTER_BYTES].any(), f"M={M}: counters left non-zero"
         assert not fresh_ws[:SPLITK_COUNTER_BYTES].any()
+
+
+# (N, K, M, epilogue): tiled-GEMM calls on long-K layers whose tiles take more
+# than one dispatch round with a part-filled last one, which the library splits
+# over K while the earlier rounds' tiles run whole.  down_proj at 4700 tokens:
+# 518 128 x 64 tiles on 512 slots, the last 6 (the partial token tile among
+# them) split 4 ways; at 10000 tokens: 553 128 x 128 tiles, the last 41 split 4
+# ways (residual epilogue); a 1152 x 2048 layer at 3700 tokens: 522 128 x 64
+# tiles, the last 10 split 4 ways (bias); a 9728 x 2048 gate|up at 800
+# tokens: 532 128 x 128 tiles, the last 20 split 4 ways (SiLU-mul).
+TAIL_SPLITS = [(896, 4864, 4700, "residual"), (896, 4864, 10000, "residual"), (1152, 2048, 3700, "bias"),
+               (9728, 2048, 800, "silu")]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("N,K,M,epi", TAIL_SPLITS, ids=[f"{n}x{k}-M{m}-{e}" for n, k, m, e in TAIL_SPLITS])
+def test_tiled_gemm_splits_the_last_rounds_tiles(dtype, N, K, M, epi):
+    """Within one rounding of the oracle (and of the unsplit call, which takes no
+    workspace), identical on a repeated call on the same workspace, and the
+    arrival counters back at zero."""
+    from nanoserve_amd.quant import splitk_workspace_bytes
+    from nanoserve_amd import _lib
+
+    lib = _lib.load()
+    assert lib.ns_int4_linear_splitk_workspace_size(M, N, K) > SPLITK_COUNTER_BYTES, "the call must split"
+    print(f"tail split N={N} K={K} M={M} {epi} {dtype}", flush=True)
+    packed, s, z = (t.to(DEV) for t in _weights(N, K, 128, N + M))
+    g = torch.Generator().manual_seed(M)
+    x = torch.randn(M, K, generator=g).to(dtype)
+    b = (torch.randn(N, generator=g) * 0.1).to(dtype) if epi == "bias" else None
+    res = torch.randn(M, N, generator=g).to(dtype) if epi == "residual" else None
+    ws = torch.zeros(splitk_workspace_bytes(N, K), dtype=torch.uint8, device=DEV)
+    kw = dict(residual=None if res is None else res.to(DEV), silu_mul=epi == "silu")
+    bd = None if b is None else b.to(DEV)
+    xd = x.to(DEV)
+    first = int4_linear(xd, packed, s, z, bd, 128, workspace=ws, **kw)
+    again = int4_linear(xd, packed, s, z, bd, 128, workspace=ws, **kw)
+    plain = int4_linear(xd, packed, s, z, bd, 128, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    assert not ws[:SPLITK_COUNTER_BYTES].any(), "arrival counters must be left at zero"
+    w = dequantize_int4_ref(packed.cpu().numpy(), s.cpu().numpy(), z.cpu().numpy(), 128, NAME[dtype])
+    y = int4_linear_ref(x.float().numpy(), w, None if b is None else b.float().numpy())
+    if epi == "silu":
+        gv, uv = _round(y[:, 0::2], dtype), _round(y[:, 1::2], dtype)
+        act = _round(gv / (1.0 + np.exp(-gv)), dtype)
+        want = _round(act * uv, dtype)
+        tol = 4 * RTOL[dtype] * np.abs(want) + 4 * RTOL[dtype] * np.abs(act * uv).max() * 1e-2 + 1e-4
+    elif epi == "residual":
+        want = _round(y, dtype) + res.double().numpy()
+        tol = 2 * RTOL[dtype] * (np.abs(y) + np.abs(res.double().numpy())) + 1e-5
+    else:
+        want = y
+        tol = RTOL[dtype] * np.abs(y) + 1e-5 * max(1.0, np.abs(y).max())
+    for t, what in ((first, "split"), (plain, "unsplit")):
+        err = np.abs(t.double().cpu().numpy() - want)
+        assert (err <= tol).all(), f"{what}: max err {err.max():.3e}"

@@ -201,18 +201,27 @@ def test_int4_linear_splitk_checks_its_workspace():
 @pytest.mark.parametrize("N,K", [(896, 4864), (896, 896), (1152, 896), (9728, 896), (4096, 8192)])
 def test_splitk_workspace_bytes_cover_every_token_count(N, K):
     """The module-level workspace (sized once per layer by a scan of token counts)
-    is at least what the library asks for at every M, through the register
-    kernel's range and the tiled GEMM's, past the point where neither splits;
-    the GEMM splits down_proj at prefill sizes (a non-zero size above 128 rows)."""
+    is at least what the library asks for at every M: densely through the
+    register kernel's range and the tiled GEMM's first rounds, then at strided and
+    odd token counts far past the scan's end (the GEMM's last-round splits
+    recur at any size).  The GEMM splits down_proj (K 4864) at prefill sizes,
+    including the part-filled last round of 4700 and 10000 tokens, and never a
+    K-896 layer (14 steps: under 8 a split); the splits only ever fill idle
+    slots of one round, so the partials never exceed 512 workgroups' 128 x 128
+    fp32 tiles."""
     from nanoserve_amd.quant import splitk_workspace_bytes
 
     lib = _lib.load()
     have = splitk_workspace_bytes(N, K)
-    sizes = [lib.ns_int4_linear_splitk_workspace_size(m, N, K) for m in range(1, 6000)]
+    rows = list(range(1, 6000)) + list(range(6007, 400_000, 997)) + [131_071, 131_073, 262_145, 1_000_003]
+    sizes = [lib.ns_int4_linear_splitk_workspace_size(m, N, K) for m in rows]
     assert max(sizes) <= have
+    assert have <= 1024 + 512 * 128 * 128 * 4
     if (N, K) == (896, 4864):
-        assert lib.ns_int4_linear_splitk_workspace_size(1024, N, K) > 0
-        assert lib.ns_int4_linear_splitk_workspace_size(2048, N, K) > 0
+        for m in (1024, 2048, 4700, 10000):
+            assert lib.ns_int4_linear_splitk_workspace_size(m, N, K) > 0
+    if K == 896:
+        assert max(sizes[128:]) == 0
 
 
 def test_int4_linear_rope_cache_rejects_bad_arguments():
