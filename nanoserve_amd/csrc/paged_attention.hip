@@ -895,6 +895,9 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
   // Positions are int32 (the host caps max_ctx below 2^31).
   const int64_t q0 = load_index(p.qsl, s, p.qsl64);
   const int64_t ql64 = load_index(p.qsl, s + 1, p.qsl64) - q0;
+  // Loaded with the query range (one round trip instead of two: c3 44.64 ->
+  // 44.49 us); s + 1 indexes query_start_loc, so s indexes seq_lens.
+  int64_t L64 = load_index(p.seq_lens, s, p.sl64);
   if (ql64 <= 0 || (p.skip_decode_rows && ql64 == 1)) return;
   if (q0 < 0 || q0 + ql64 > p.num_tokens) return;
   const int64_t ncols = ql64 * G;
@@ -916,7 +919,6 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
   }
   const int64_t c_wg = cb * Cfg::COLS;
   if (c_wg >= ncols) return;
-  int64_t L64 = load_index(p.seq_lens, s, p.sl64);
   L64 = L64 < p.max_ctx ? L64 : p.max_ctx;
   const int L = static_cast<int>(L64 > 0 ? L64 : 0);
   const int64_t ctx0 = L - ql64;  // absolute position of query row 0 (may be negative)
