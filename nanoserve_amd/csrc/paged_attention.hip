@@ -967,15 +967,27 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
   }
   const float sc = fabsf(p.scale_log2);
 
+  // Running softmax state per column: maximum, the row sum of P, and O^T.
+  // The row sum runs on the matrix cores: one more PV product whose V^T
+  // operand is a row of ones (row 0 of the tile, every key) puts sum_k P[k]
+  // of column c16 in element 0 of lane (g = 0, c16) and zero everywhere else,
+  // which is this lane's share of the column's sum as group4_sum_swap adds
+  // them up at the end.  It sums the same half-precision P that the PV
+  // product weighs V with, and takes 16 VALU adds per column tile and step
+  // off the softmax.
   float m_run[CT], l_run[CT];
-  floatx4 acc[CT][NN];
+  floatx4 acc[CT][NN], lacc[CT];
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     m_run[ct] = -INFINITY;
     l_run[ct] = 0.f;
+    lacc[ct] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int n = 0; n < NN; ++n) acc[ct][n] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
+  V8 ones_row;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ones_row[e] = static_cast<T>(c16 == 0 ? 1.f : 0.f);
 
   const int64_t slot_stride = static_cast<int64_t>(Hkv) * D;
   const int64_t bt_row = static_cast<int64_t>(s) * p.bt_stride;
@@ -1091,16 +1103,12 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
 #pragma unroll
           for (int r = 0; r < 4; ++r) sv[j][r] = fast_exp2(sv[j][r] - msub);
       }
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < NT; ++j)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) psum += sv[j][r];
-      l_run[ct] = l_run[ct] * alpha + psum;
-      // Rescale only when some column's maximum moved (alpha == 1 is exact).
+      // Rescale only when some column's maximum moved (alpha == 1 is exact);
+      // the row sum's other elements stay zero.
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
         for (int n = 0; n < NN; ++n) acc[ct][n] *= alpha;
+        lacc[ct][0] *= alpha;
       }
       m_run[ct] = m_new;
 #pragma unroll
@@ -1138,9 +1146,11 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
           }
       }
 #pragma unroll
-      for (int pb = 0; pb < NT / 2; ++pb)
+      for (int pb = 0; pb < NT / 2; ++pb) {
 #pragma unroll
         for (int n = 0; n < NN; ++n) acc[ct][n] = mfma16x16x32(DT{}, va[pb][n], pt[ct][pb], acc[ct][n]);
+        lacc[ct] = mfma16x16x32(DT{}, ones_row, pt[ct][pb], lacc[ct]);
+      }
     }
   };
 
@@ -1201,6 +1211,8 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   __syncthreads();  // every group's steps are done; the ring is free
+#pragma unroll
+  for (int ct = 0; ct < CT; ++ct) l_run[ct] = lacc[ct][0];
   const int need_w = (kv_end_w + bs_mask) >> bs_shift;
   const bool bad_w = *bad_first < need_w;
 
