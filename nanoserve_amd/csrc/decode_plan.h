@@ -63,6 +63,13 @@ constexpr int kMaxItemTokens = 4096;
 // kept few and items long; the longest-first order balances what is left.
 inline int plan_min_tokens(int head_dim) { return head_dim == 64 ? 128 : 64; }
 inline int plan_round_tokens(int head_dim) { return head_dim == 64 ? 4096 : 2048; }
+// One-round plans keep items at least this long (0: no such floor) while the
+// batch still gives half of the CUs an item at that length: shorter items then
+// add split-K merges faster than they add streaming CUs (c2, B = 32 around 1k
+// tokens: 12.31 -> 12.19 us per call with 512-token items), and batches that
+// need the short items' parallelism (the c5 engine's decode steps, under half
+// the CUs at 512 tokens) keep them.
+inline int plan_long_tokens(int head_dim) { return head_dim == 64 ? 512 : 0; }
 
 // Rounds of items per CU the decode grid provides for a batch whose work is at
 // most num_seqs * num_kv_heads * max_ctx tokens (the host does not know the
@@ -107,7 +114,7 @@ struct DecodePlanArgs {
   int64_t max_ctx;  // lengths are clamped to this (tokens addressable through a table row)
   int cus;          // CUs of the device, at most kPlanCUs
   int rounds;       // upper bound on items per CU (plan_max_rounds)
-  int min_tokens, round_tokens;
+  int min_tokens, round_tokens, long_tokens;
 };
 
 // Launch the (single-workgroup) plan kernel on `stream`.

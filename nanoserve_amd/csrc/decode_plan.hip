@@ -9,6 +9,8 @@
 //    host's bound); when even the largest T (the longest context, at most
 //    kMaxItemTokens) does not fit, T is that largest value.  Sequence s is
 //    cut into n_s = max(1, ceil(L_s / T)) ranges of equal 16-aligned size.
+//    A one-round plan raises T to long_tokens when the batch still has at
+//    least half as many items as CUs at that length.
 // 3. Pairs are listed longest sequence first (so the dispatcher starts the
 //    long pairs, whose merges finish last, first), the n_s items of each
 //    (sequence, kv head) pair next to each other.
@@ -198,7 +200,25 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
       ca += m * step + 1;
     }
   }
-  const uint32_t T = static_cast<uint32_t>(ca * 16);
+  uint32_t T = static_cast<uint32_t>(ca * 16);
+  // One-round plans: items of long_tokens when they still give half of the
+  // CUs an item (fewer, longer items: fewer split-K merges).
+  if (rounds == 1 && T < static_cast<uint32_t>(a.long_tokens)) {
+    const uint32_t TL = static_cast<uint32_t>(a.long_tokens);
+    uint32_t nl = 0;
+    for (int s = tid; s < S; s += kThreads) {
+      const int32_t L = lens[s];
+      if (L >= 0) nl += items_of(static_cast<uint32_t>(L), TL);
+    }
+    nl = __ockl_wfred_add_u32(nl);
+    if (lane == 0) sh.red[w] = nl;
+    __syncthreads();
+    nl = 0;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) nl += sh.red[k];
+    __syncthreads();  // red is reused below
+    if (2 * static_cast<int64_t>(nl) * Hkv >= a.cus) T = TL;
+  }
 
   // 3. List order.  When every item runs at once (at most `cus` items) the
   // order does not matter and the batch's own order is kept; otherwise

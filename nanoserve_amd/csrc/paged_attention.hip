@@ -1491,6 +1491,7 @@ DecodePlanArgs plan_args(void* plan, int64_t item_cap, const void* block_tables,
   a.rounds = d.rounds;
   a.min_tokens = plan_min_tokens(head_dim);
   a.round_tokens = plan_round_tokens(head_dim);
+  a.long_tokens = plan_long_tokens(head_dim);
   return a;
 }
 

@@ -123,6 +123,22 @@ def test_plan_of_config_like_decode_batches(index_dtype):
     _check(c4, [1] * 64, hkv=4, d=128, index_dtype=index_dtype)
 
 
+def test_one_round_plans_keep_long_items_while_half_the_cus_get_one():
+    """A one-round D=64 plan takes 512-token items when the batch still has at
+    least half as many items as CUs at that length (fewer split-K merges), and
+    keeps shorter items when it would not (the parallelism is needed)."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    rng = np.random.default_rng(0)
+    c2 = np.clip(rng.lognormal(np.log(1024), 0.8, 32).astype(int), 16, 8192).tolist()
+    at512 = 2 * sum(max(1, -(-L // 512)) for L in c2)
+    T, n = _check(c2, [1] * 32)
+    if 2 * at512 >= min(cus, 256):
+        assert T == 512 and n == at512
+    short = [400] * 32  # 64 items at 512 tokens: under half of the CUs
+    T, n = _check(short, [1] * 32)
+    assert T < 512 and n > 64
+
+
 def test_plan_edge_cases():
     _check([0, 0, 5], [1, 1, 1])                       # empty contexts
     _check([1], [1])                                   # a single token
