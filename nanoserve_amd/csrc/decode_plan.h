@@ -66,9 +66,11 @@ inline int plan_round_tokens(int head_dim) { return head_dim == 64 ? 4096 : 2048
 // One-round plans keep items at least this long (0: no such floor) while the
 // batch still gives half of the CUs an item at that length: shorter items then
 // add split-K merges faster than they add streaming CUs (c2, B = 32 around 1k
-// tokens: 12.31 -> 12.19 us per call with 512-token items), and batches that
+// tokens: 12.31 -> 12.23 us per call with 512-token items), and batches that
 // need the short items' parallelism (the c5 engine's decode steps, under half
-// the CUs at 512 tokens) keep them.
+// the CUs at 512 tokens) keep them.  A batch whose every context fits one
+// such item takes it too: no split-K merge at all (c1, B = 8 up to 512
+// tokens: 8.59 -> 8.16 us; B = 8 / 32 at 512 tokens: -13% / -9%).
 inline int plan_long_tokens(int head_dim) { return head_dim == 64 ? 512 : 0; }
 
 // Rounds of items per CU the decode grid provides for a batch whose work is at

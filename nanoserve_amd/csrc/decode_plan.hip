@@ -10,7 +10,8 @@
 //    kMaxItemTokens) does not fit, T is that largest value.  Sequence s is
 //    cut into n_s = max(1, ceil(L_s / T)) ranges of equal 16-aligned size.
 //    A one-round plan raises T to long_tokens when the batch still has at
-//    least half as many items as CUs at that length.
+//    least half as many items as CUs at that length, or when every context
+//    fits one item of that length.
 // 3. Pairs are listed longest sequence first (so the dispatcher starts the
 //    long pairs, whose merges finish last, first), the n_s items of each
 //    (sequence, kv head) pair next to each other.
@@ -202,7 +203,8 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
   }
   uint32_t T = static_cast<uint32_t>(ca * 16);
   // One-round plans: items of long_tokens when they still give half of the
-  // CUs an item (fewer, longer items: fewer split-K merges).
+  // CUs an item (fewer, longer items: fewer split-K merges), or when every
+  // context fits one such item (no split-K merge at all).
   if (rounds == 1 && T < static_cast<uint32_t>(a.long_tokens)) {
     const uint32_t TL = static_cast<uint32_t>(a.long_tokens);
     uint32_t nl = 0;
@@ -217,7 +219,7 @@ __global__ __launch_bounds__(kThreads) void decode_plan_kernel(DecodePlanArgs a,
 #pragma unroll
     for (int k = 0; k < kWaves; ++k) nl += sh.red[k];
     __syncthreads();  // red is reused below
-    if (2 * static_cast<int64_t>(nl) * Hkv >= a.cus) T = TL;
+    if (2 * static_cast<int64_t>(nl) * Hkv >= a.cus || max_len <= TL) T = TL;
   }
 
   // 3. List order.  When every item runs at once (at most `cus` items) the

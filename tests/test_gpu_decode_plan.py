@@ -125,8 +125,9 @@ def test_plan_of_config_like_decode_batches(index_dtype):
 
 def test_one_round_plans_keep_long_items_while_half_the_cus_get_one():
     """A one-round D=64 plan takes 512-token items when the batch still has at
-    least half as many items as CUs at that length (fewer split-K merges), and
-    keeps shorter items when it would not (the parallelism is needed)."""
+    least half as many items as CUs at that length (fewer split-K merges) or
+    when every context fits one such item (no merge at all), and keeps shorter
+    items otherwise (the parallelism is needed)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     rng = np.random.default_rng(0)
     c2 = np.clip(rng.lognormal(np.log(1024), 0.8, 32).astype(int), 16, 8192).tolist()
@@ -134,9 +135,12 @@ def test_one_round_plans_keep_long_items_while_half_the_cus_get_one():
     T, n = _check(c2, [1] * 32)
     if 2 * at512 >= min(cus, 256):
         assert T == 512 and n == at512
-    short = [400] * 32  # 64 items at 512 tokens: under half of the CUs
-    T, n = _check(short, [1] * 32)
-    assert T < 512 and n > 64
+    single = [400] * 32  # every context fits one 512-token item
+    T, n = _check(single, [1] * 32)
+    assert T == 512 and n == 64
+    mixed = [400] * 31 + [900]  # 66 items at 512 tokens and one pair split: short items
+    T, n = _check(mixed, [1] * 32)
+    assert T < 512 and n > 66
 
 
 def test_plan_edge_cases():
