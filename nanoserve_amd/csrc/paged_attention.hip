@@ -789,6 +789,20 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     if (idx < n_items) load_item(p, idx, r0, r1, ib);
     __syncthreads();  // the next item reuses the LDS
   }
+  // The next call of a step (every layer uses the step's plan) starts this
+  // workgroup index on the same XCD (blockIdx mod 8), reading the same first
+  // item and the header: read them once more now, with vector loads, so they
+  // sit in this XCD's L2 (c2 12.23 -> 12.15 us per call, c1 8.17 -> 8.09).
+  // Read-only and inside the plan buffer (the grid never exceeds its
+  // capacity).
+  if (threadIdx.x < 11) {
+    const u32x4* rows = reinterpret_cast<const u32x4*>(p.items + blockIdx.x);
+    const void* ptr = threadIdx.x < 10 ? static_cast<const void*>(rows + threadIdx.x)
+                                       : static_cast<const void*>(p.plan_hdr);
+    u32x4 v;
+    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 }
 
 // --------------------------------------------------------------------------
