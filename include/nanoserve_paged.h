@@ -293,7 +293,9 @@ size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads, int num_kv
  * one-query-row sequences of a mixed batch, found from query_start_loc)
  * into items of context tokens of one (sequence, kv head) pair, sized so
  * the items about fill the device once for light batches and in several
- * rounds, longest sequences first, for heavy ones.  Each item also carries
+ * rounds, longest sequences first, for heavy ones; at head_dim 64 a
+ * one-round plan keeps items of 512 tokens while that still gives half of
+ * the CUs an item or every context fits one item.  Each item also carries
  * the block ids of its waves' first K/V loads (block size >= 16), so those
  * loads need no table round trip.  It reads only device memory (seq_lens,
  * query_start_loc, block_tables), so a captured HIP graph rebuilds it from
