@@ -1354,7 +1354,24 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     if (tid == 0) __hip_atomic_store(&p.pf_counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  if (kg != 0 || !wave_on) return;
+  if (kg != 0 || !wave_on) {
+    // While group 0 stores the outputs, one wave of group 1 reads the
+    // workgroup's block-table entries once more: the next call of the step
+    // (every layer shares the step's tables) starts this workgroup index on
+    // the same XCD and finds its table window in that XCD's L2 (c3 43.95 ->
+    // 43.73 us).  Read-only, the entries the window loads above read.
+    if (kg == 1 && wc == 0) {
+      const int e_end = (kv_end + bs_mask) >> bs_shift;
+      const int e_beg = (M_begin * MKEYS) >> bs_shift;
+      for (int e = e_beg + lane; e < e_end; e += 64) {
+        const char* a = static_cast<const char*>(p.bt) + (bt_row + e) * static_cast<int64_t>(sizeof(BTI));
+        uint32_t v;
+        asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a) : "memory");
+      }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
+    return;
+  }
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float lsum = group4_sum_swap(l_run[ct]);
