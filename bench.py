@@ -177,6 +177,13 @@ def _copy_calibration(torch, mb):
     return 0
 
 
+def graph_capture(graph, stream=None, pool=None):
+    """nanoserve_amd.capture.graph_capture (imported on use: torch loads late here)."""
+    from nanoserve_amd.capture import graph_capture as capture
+
+    return capture(graph, stream=stream, pool=pool)
+
+
 def _graph_time(torch, stream, launch, n, reps=3):
     """Seconds per launch of `launch(i)` for i in [0, n), captured in one HIP
     graph and replayed (best of `reps` timed replays after one warm replay)."""
@@ -185,7 +192,7 @@ def _graph_time(torch, stream, launch, n, reps=3):
             launch(i)
     stream.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
+    with graph_capture(g, stream=stream):
         for i in range(n):
             launch(i)
     best = float("inf")
@@ -494,17 +501,15 @@ def _time_steps(torch, steps, news, K, warmup, stream):
     steps once, so the timed calls are exactly K * calls-per-step calls and
     their bytes are summed exactly."""
     from nanoserve_amd import paged_attention_hip, reshape_and_cache, rope_reshape_and_cache
-    from nanoserve_amd.attention import prepare_decode_plan
 
     calls = [c for st in steps for c in st]
     R, L = len(steps), len(steps[0])
 
     def attn(i):
+        # The reference's call site unchanged (qwen2.py:59-65): one call per
+        # layer with the step's shared metadata and no per-step hook; the
+        # step's first call builds the device-side decode plan on its md.
         c = calls[i]
-        # A step's metadata gets its device-side decode plan once, before its
-        # first layer's call, as the model's forward does (Qwen2Model.forward).
-        if i == 0 or c.md is not calls[i - 1].md:
-            prepare_decode_plan(c.md, c.k_cache)
         return paged_attention_hip(c.query, c.k_cache, c.v_cache, c.md, c.scale)
 
     def write(i):
@@ -531,7 +536,7 @@ def _time_steps(torch, steps, news, K, warmup, stream):
 
     def capture(fn):
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=stream):
+        with graph_capture(g, stream=stream):
             fn()
         return g
 
@@ -617,13 +622,12 @@ def _time_attn_variant(torch, steps, K, stream, per_step_plan=True, host_lists=T
     """Microseconds per attention call of K graph-replayed serving steps, for
     the variants the line reports beside its main figure: the step's metadata
     without any host-side lengths (host_lists=False: the engine's graph
-    replays, which never pass host copies), and every call building its own
-    decode plan (per_step_plan=False: a caller that does not share one plan
-    across the layers of a step)."""
+    replays, which never pass host copies), and every call planning its decode
+    rows inside the call (per_step_plan=False: a caller whose layers do not
+    share one plan, e.g. one that builds a new metadata object per call)."""
     import dataclasses
 
-    from nanoserve_amd import paged_attention_hip
-    from nanoserve_amd.attention import prepare_decode_plan
+    from nanoserve_amd.attention import _attention
 
     mds = {}
     for st in steps:
@@ -639,16 +643,14 @@ def _time_attn_variant(torch, steps, K, stream, per_step_plan=True, host_lists=T
         for j in range(n):
             for i in range(j * L, (j + 1) * L):
                 c, md = calls[i]
-                if per_step_plan and i == j * L:
-                    prepare_decode_plan(md, c.k_cache)
-                paged_attention_hip(c.query, c.k_cache, c.v_cache, md, c.scale)
+                _attention(c.query, c.k_cache, c.v_cache, md, c.scale, share_plan=per_step_plan)
 
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
         run(R)
     stream.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=stream):
+    with graph_capture(g, stream=stream):
         run(R)
     reps = max(1, -(-K // R))
     with torch.cuda.stream(stream):
@@ -769,10 +771,11 @@ def main(argv=None):
         },
         "no_host_plan_us": round(no_host_us, 3),
         "per_call_plan_us": round(per_call_plan_us, 3),
-        "plan_note": "the decode plan is built on the device from seq_lens in every variant: us_per_call and "
-                     "no_host_plan_us build it once per step (no_host_plan_us with the metadata's host-side "
-                     "lengths removed, as the engine's graph replays run); per_call_plan_us builds it inside "
-                     "every attention call",
+        "plan_note": "the decode plan is built on the device from seq_lens in every variant: us_per_call "
+                     "calls paged_attention_hip as the reference's qwen2.py does (one md per step, no per-step "
+                     "hook), so the step's first call builds the plan and the other layers reuse it; "
+                     "no_host_plan_us does the same with the metadata's host-side lengths removed (as the "
+                     "engine's graph replays run); per_call_plan_us plans inside every attention call",
         "reshape_and_cache_us": round(res["write_us"], 3),
         "rope_reshape_and_cache": {
             "us_per_call": round(res["rope_us"], 3),

@@ -149,6 +149,7 @@ SIGNATURES = {
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
+_capture_info = None
 
 
 def load() -> ctypes.CDLL:
@@ -177,3 +178,22 @@ def check(rc: int, what: str) -> None:
     if rc != NS_OK:
         msg = load().ns_error_string(rc).decode()
         raise RuntimeError(f"{what} failed: {msg} (status {rc})")
+
+
+def stream_capture_id(stream: int) -> int:
+    """The id of the graph capture under way on `stream` (a hipStream_t as an
+    int), or 0 when the stream is not capturing.
+
+    Read with the HIP runtime's hipStreamGetCaptureInfo from the copy torch
+    loaded (the library's own dependency resolves to it, see the top)."""
+    global _capture_info
+    if _capture_info is None:
+        fn = ctypes.CDLL("libamdhip64.so.7").hipStreamGetCaptureInfo
+        fn.restype = c_int
+        fn.argtypes = [c_void_p, ctypes.POINTER(c_int), ctypes.POINTER(ctypes.c_ulonglong)]
+        _capture_info = fn
+    status, cid = c_int(0), ctypes.c_ulonglong(0)
+    rc = _capture_info(c_void_p(stream), ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed with HIP error {rc}")
+    return int(cid.value) if status.value == 1 else 0  # 1: hipStreamCaptureStatusActive

@@ -8,11 +8,19 @@ sequence with context length L and query length ql attends to keys
 [0, L - ql + j]; the kv head of query head h is h // (Hq // Hkv).
 
 Everything runs on the GPU through libnanoserve_paged.so: the decode rows of a
-batch are one kernel launch over a work plan built on the device (once per
-step with `prepare_decode_plan`, else by the call itself), with split-K
-partials merged inside the launch; any other batch adds one launch of the
-variable-length MFMA kernel.  There is no torch or Triton fallback; a missing
-library or an unsupported shape raises.
+batch are one kernel launch over a work plan built on the device, with
+split-K partials merged inside the launch; any other batch adds one launch of
+the variable-length MFMA kernel.  There is no torch or Triton fallback; a
+missing library or an unsupported shape raises.
+
+The plan belongs to the step, like the metadata: the reference builds one
+AttentionMetadata per step and hands the same object to every layer
+(model_runner.py:85-147, qwen2.py:105-113), so the first call that sees an
+`md` builds its plan (one small launch) and stores it on the `md`; the other
+layers' calls find it there.  A caller that rewrites an md's device tensors in
+place for a new step must clear `md.decode_plan` (or call
+`prepare_decode_plan` again); the engine builds a new md per step, and a
+captured graph rebuilds the plan in every replay.
 """
 
 from __future__ import annotations
@@ -47,17 +55,21 @@ class AttentionMetadata:
     query_lens_cpu: list[int] = None          # type: ignore[assignment]
     seq_lens_cpu: list[int] = None            # type: ignore[assignment]
     query_start_loc_cpu: list[int] = None     # type: ignore[assignment]
-    # The step's device-side decode plan (prepare_decode_plan), built once and
-    # read by every layer's call; None makes each call build its own.
+    # The step's device-side decode plan (prepare_decode_plan), built by the
+    # step's first attention call (or explicitly before it) and read by every
+    # layer's call.
     decode_plan: "DecodePlan | None" = None
 
 
 @dataclass(frozen=True)
 class DecodePlan:
-    """A device buffer holding ns_paged_decode_plan's output, and the call sizes it is valid for."""
+    """A device buffer holding ns_paged_decode_plan's output, the call sizes it
+    is valid for, and the graph capture that built it (0: none).  A plan built
+    inside a capture is written by that graph's replays only."""
 
     buffer: torch.Tensor
     key: tuple
+    capture: int = 0
 
 
 _INDEX_DTYPES = (torch.int32, torch.int64)
@@ -67,6 +79,16 @@ _INDEX_DTYPES = (torch.int32, torch.int64)
 # a cached buffer is reused without clearing.  Calls on different streams may
 # overlap in time and therefore get different buffers.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Buffers a larger one replaced.  A graph captured while one of them was
+# current still holds its address, so they stay allocated for the process
+# (torch hands out recycled stream handles, so a key can also be reused by a
+# later, unrelated stream).  Growth is geometric: they add up to less than
+# the current buffer.
+_retired: list[torch.Tensor] = []
+# Plans built inside a graph capture and later replaced on their md (the md
+# was used again eagerly or in another capture): the graph still writes and
+# reads the buffer on every replay, so it is never freed.
+_captured_plans: list["DecodePlan"] = []
 
 # Per (device, stream): the second stream and fork/join events a mixed batch
 # overlaps its decode launch on.  The shim owns them; the library only uses
@@ -92,6 +114,8 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
                 "once on this stream before capturing")
         # Grow geometrically so a slowly growing max_seq_len reallocates rarely.
         size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
+        if ws is not None:
+            _retired.append(ws)
         ws = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws
@@ -124,11 +148,15 @@ def _index(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
 
 def _plan_key(md: AttentionMetadata, num_kv_heads: int, head_dim: int, block_size: int,
               device: torch.device) -> tuple:
-    """What a plan depends on besides the device lengths it reads: the call sizes
-    and the metadata tensors it was built from."""
+    """What a plan depends on besides the device lengths it reads: the call sizes,
+    the metadata tensors it was built from and, when the metadata carries them,
+    the host copies of the lengths and query offsets."""
+    lens = None if md.seq_lens_cpu is None else tuple(md.seq_lens_cpu[:md.num_seqs])
+    qsl = None if md.is_decode_only or md.query_start_loc_cpu is None else tuple(md.query_start_loc_cpu)
     return (md.num_seqs, num_kv_heads, head_dim, block_size, md.max_seq_len, int(md.block_tables.shape[1]),
             bool(md.is_decode_only), md.seq_lens.data_ptr(),
-            None if md.query_start_loc is None else md.query_start_loc.data_ptr(), _device_index(device))
+            None if md.query_start_loc is None else md.query_start_loc.data_ptr(), _device_index(device),
+            lens, qsl)
 
 
 @torch.inference_mode()
@@ -165,7 +193,12 @@ def prepare_decode_plan(md: AttentionMetadata, cache: torch.Tensor) -> None:
                                   qsl_ptr, qsl64, md.num_seqs, int(decode_only), num_kv_heads, head_dim,
                                   block_size, md.max_seq_len, torch.cuda.current_stream(device).cuda_stream)
     _lib.check(rc, "ns_paged_decode_plan")
-    md.decode_plan = DecodePlan(buf, _plan_key(md, num_kv_heads, head_dim, block_size, device))
+    stream = torch.cuda.current_stream(device).cuda_stream
+    capture = _lib.stream_capture_id(stream) if torch.cuda.is_current_stream_capturing() else 0
+    old = md.decode_plan
+    if old is not None and old.capture not in (0, capture):
+        _captured_plans.append(old)
+    md.decode_plan = DecodePlan(buf, _plan_key(md, num_kv_heads, head_dim, block_size, device), capture)
 
 
 def workspace_bytes(md: AttentionMetadata, num_heads: int, num_kv_heads: int,
@@ -184,7 +217,17 @@ def paged_attention_hip(
     md: AttentionMetadata,
     scale: float,
 ) -> torch.Tensor:
-    """Unified paged attention on the GPU.  Returns [num_tokens, num_heads, head_dim]."""
+    """Unified paged attention on the GPU.  Returns [num_tokens, num_heads, head_dim].
+
+    The reference's attn_fn contract (attention.py:99-151).  The decode plan
+    is shared by the calls of one md: built by the first, reused by the rest."""
+    return _attention(query, k_cache, v_cache, md, scale, share_plan=True)
+
+
+def _attention(query, k_cache, v_cache, md: AttentionMetadata, scale: float, share_plan: bool) -> torch.Tensor:
+    """paged_attention_hip's body.  share_plan=False leaves md.decode_plan
+    unused and untouched: the library then plans the decode rows inside the
+    call (in its workspace)."""
     lib = _lib.load()
     if query.dim() != 3 or k_cache.dim() != 4 or v_cache.shape != k_cache.shape:
         raise ValueError(
@@ -256,9 +299,22 @@ def paged_attention_hip(
             f"block_size={block_size}")
     ws = _workspace(device, stream, nbytes)
     aux = (None, None, None) if decode_only else _aux_stream(device, stream)
-    plan = md.decode_plan
-    if plan is not None and plan.key != _plan_key(md, num_kv_heads, head_dim, block_size, device):
-        plan = None  # built for other sizes: the call plans for itself
+    plan = None
+    # A batch whose host offsets show no one-row sequence has no decode rows:
+    # the library launches no decode kernel and needs no plan.
+    has_decode_rows = decode_only or qsl_host is None or lens_host is None or any(
+        b - a == 1 for a, b in zip(md.query_start_loc_cpu[:md.num_seqs], md.query_start_loc_cpu[1:md.num_seqs + 1]))
+    if share_plan and has_decode_rows:
+        # Reuse md's plan only in the context that built it: eagerly, or inside
+        # the same graph capture (whose replays rebuild it).  Anywhere else
+        # this call builds the step's plan anew; a replaced plan that a
+        # captured graph owns stays allocated for that graph.
+        capture = _lib.stream_capture_id(stream) if torch.cuda.is_current_stream_capturing() else 0
+        plan = md.decode_plan
+        if plan is None or plan.capture != capture or \
+                plan.key != _plan_key(md, num_kv_heads, head_dim, block_size, device):
+            prepare_decode_plan(md, k_cache)  # this step's first call here (or md changed shape)
+            plan = md.decode_plan
 
     rc = lib.ns_paged_attention(
         out.data_ptr(), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),

@@ -21,6 +21,7 @@ import torch
 
 from .attention import AttentionMetadata, get_attention_backend
 from .block_manager import BlockSpaceManager
+from .capture import no_cycle_collection
 from .kv_cache import PagedKVCache
 from .sampling import argmax_rows
 from .scheduling import RequestMetrics, SamplingParams, Scheduler, SchedulerConfig, Sequence, SeqState
@@ -138,10 +139,24 @@ class DecodeGraphs:
     ids are then gathered on the device from this step's greedy output.  Two
     pinned staging buffers alternate, so filling step N+1 never overwrites the
     buffer step N's copy may still be reading.
+
+    Lifetimes.  The object keeps the runner's model, cache and attention
+    function but not the runner itself, so an engine and its graphs form no
+    reference cycle and are freed as soon as the engine is dropped, not by a
+    later cycle collection (which could otherwise run inside another graph's
+    capture; see `capture.no_cycle_collection`).  Each graph is kept with the
+    metadata it was captured with, so the step's decode-plan buffer -- a
+    tensor of the graph's private pool that every replay rewrites and reads
+    -- stays allocated for the graph's lifetime and is never handed to a
+    later capture.
     """
 
     def __init__(self, runner: "ModelRunner", sizes: tuple[int, ...], max_model_len: int) -> None:
-        self.runner = runner
+        self.model = runner.model
+        self.kv_cache = runner.kv_cache
+        self.attn_fn = runner.attn_fn
+        self.block_size = runner.block_size
+        self.device = runner.device
         self.sizes = sorted(sizes)
         self.max_model_len = max_model_len
         self.width = -(-max_model_len // runner.block_size)
@@ -162,7 +177,7 @@ class DecodeGraphs:
         # valid entries and a decode step writes only blocks added since.
         # Holding the lists keeps their ids from reuse.
         self._rows: list[tuple[int, list[tuple[list, int]]]] = [(0, []), (0, [])]
-        self._graphs: dict[tuple[int, int], tuple[torch.cuda.CUDAGraph, torch.Tensor, torch.Tensor]] = {}
+        self._graphs: dict[tuple[int, int], CapturedStep] = {}
         self.last_logits: torch.Tensor | None = None  # graph-owned logits of the latest replay
         self._pool = None
         self._stream = torch.cuda.Stream(runner.device) if runner.device.type == "cuda" else None
@@ -172,7 +187,7 @@ class DecodeGraphs:
                 and all(s.num_tokens <= self.max_model_len for s, _ in scheduled))
 
     def _table_width(self, ctx: int) -> int:
-        return -(-ctx // self.runner.block_size)
+        return -(-ctx // self.block_size)
 
     def _views(self, b: int, ctx: int):
         n, w = max(self.sizes), self._table_width(ctx)
@@ -198,7 +213,7 @@ class DecodeGraphs:
         padding rows get slot -1 (no cache write), length 1 and block 0.
         With `gather`, row i's token is not known on the host yet and is row
         gather[i] of the previous launch's greedy output."""
-        n, bs, w = max(self.sizes), self.runner.block_size, self._table_width(ctx)
+        n, bs, w = max(self.sizes), self.block_size, self._table_width(ctx)
         slot_i = self._next
         self._next ^= 1
         h = self._host_np[slot_i]
@@ -242,16 +257,16 @@ class DecodeGraphs:
         return slot_i
 
     def _capture(self, b: int, ctx: int):
-        r = self.runner
         ids, pos, md = self._metadata(b, ctx)
+        model, kv_cache, attn_fn = self.model, self.kv_cache, self.attn_fn
 
         def forward():
-            hidden = r.model(ids, pos, r.kv_cache, md, r.attn_fn)
-            logits = r.model.compute_logits(hidden)
+            hidden = model(ids, pos, kv_cache, md, attn_fn)
+            logits = model.compute_logits(hidden)
             return argmax_rows(logits), logits
 
         s = self._stream
-        s.wait_stream(torch.cuda.current_stream(r.device))
+        s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):  # warm-up: workspaces and allocator state for this stream
             forward()
             forward()
@@ -261,17 +276,22 @@ class DecodeGraphs:
             out, logits = forward()
         if self._pool is None:
             self._pool = g.pool()
-        self._graphs[(b, ctx)] = (g, out, logits)
+        self._graphs[(b, ctx)] = CapturedStep(g, out, logits, md)
 
     def capture_all(self) -> None:
-        """Capture every bucket up front, largest first (the pool then fits the rest)."""
+        """Capture every bucket up front, largest first (the pool then fits the rest).
+
+        The cycle collector is held off for the whole sequence (pending
+        garbage is collected first), so no destructor of unrelated objects
+        runs inside a capture."""
         self._dev.zero_()
         self._dev[3 * max(self.sizes):4 * max(self.sizes)] = 1
         self._dev[2 * max(self.sizes):3 * max(self.sizes)] = -1
-        for ctx in sorted(self.ctx_sizes, reverse=True):
-            for b in sorted(self.sizes, reverse=True):
-                if (b, ctx) not in self._graphs:
-                    self._capture(b, ctx)
+        with no_cycle_collection():
+            for ctx in sorted(self.ctx_sizes, reverse=True):
+                for b in sorted(self.sizes, reverse=True):
+                    if (b, ctx) not in self._graphs:
+                        self._capture(b, ctx)
 
     @torch.inference_mode()
     def launch(self, scheduled, after: "GraphLaunch | None" = None) -> "GraphLaunch":
@@ -282,7 +302,8 @@ class DecodeGraphs:
         ctx = next(c for c in self.ctx_sizes if c >= longest)
         if (b, ctx) not in self._graphs:
             self.capture_all()
-        g, out, logits = self._graphs[(b, ctx)]
+        step = self._graphs[(b, ctx)]
+        g, out, logits = step.graph, step.out, step.logits
         gather = None
         if after is not None:
             where = {seq.seq_id: i for i, (seq, _) in enumerate(after.scheduled)}
@@ -312,6 +333,17 @@ class DecodeGraphs:
         for seq, q in scheduled:
             seq.mark_computed(q)
         return [(seq, tok) for (seq, _), tok in zip(scheduled, tokens)]
+
+
+@dataclass
+class CapturedStep:
+    """One captured decode step: the graph, its static outputs, and the
+    metadata (with the decode-plan buffer) its kernels were captured with."""
+
+    graph: torch.cuda.CUDAGraph
+    out: torch.Tensor        # greedy token per row
+    logits: torch.Tensor     # [bucket, vocab]
+    md: AttentionMetadata    # keeps md.decode_plan's buffer allocated
 
 
 @dataclass

@@ -14,6 +14,9 @@ from . import _lib
 # One slice-key workspace per (device, stream), grown on demand; graph capture
 # records its pointer, so it is allocated by the warm-up call before capture.
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+# Buffers a larger one replaced: a graph captured with one of them keeps its
+# address (and torch recycles stream handles), so they are never freed.
+_retired: list[torch.Tensor] = []
 
 
 def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
@@ -27,6 +30,8 @@ def _workspace(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
                 f"argmax_rows needs a {nbytes}-byte workspace on stream {stream:#x} during graph "
                 f"capture, but has {0 if ws is None else ws.numel()} bytes: run the largest shape "
                 "once on this stream before capturing")
+        if ws is not None:
+            _retired.append(ws)
         ws = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
         _workspaces[key] = ws
     return ws

@@ -121,3 +121,56 @@ def test_random_init_is_seeded_and_tied():
     for (n1, p1), (_, p2) in zip(a.named_parameters(), b.named_parameters()):
         assert torch.equal(p1, p2), n1
     assert torch.equal(a.model.layers[0].input_layernorm.weight, torch.ones(256))
+
+
+# ---- object lifetimes around graph capture ----------------------------------
+def test_an_engine_with_decode_graphs_is_freed_without_the_cycle_collector():
+    """Dropping an engine frees its decode graphs (and their pinned staging
+    buffers) at once, by reference counting.  Were the graphs and the runner
+    to reference each other, they would live until some later cycle
+    collection, which may run inside another engine's graph capture: freeing
+    a pinned buffer that served a non_blocking copy records an event on the
+    copy's stream, which HIP refuses during a capture, and the process
+    aborts."""
+    import gc
+    import weakref
+
+    from nanoserve_amd.engine import LLMEngine
+
+    model = Qwen2ForCausalLM(Qwen2Config(**TINY))
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        eng = LLMEngine(model, num_blocks=16, block_size=8, device="cpu", max_model_len=256, use_graphs=True)
+        graphs = weakref.ref(eng.runner.graphs)
+        runner = weakref.ref(eng.runner)
+        del eng
+        assert graphs() is None and runner() is None
+    finally:
+        if was:
+            gc.enable()
+
+
+def test_no_cycle_collection_collects_first_and_holds_the_collector_off():
+    import gc
+    import weakref
+
+    from nanoserve_amd.capture import no_cycle_collection
+
+    class Node:
+        pass
+
+    a, b = Node(), Node()
+    a.other, b.other = b, a  # a cycle only the collector can free
+    dead = weakref.ref(a)
+    del a, b
+    was = gc.isenabled()
+    gc.enable()
+    try:
+        with no_cycle_collection():
+            assert dead() is None  # collected on entry, before any capture starts
+            assert not gc.isenabled()
+        assert gc.isenabled()
+    finally:
+        if not was:
+            gc.disable()

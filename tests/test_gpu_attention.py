@@ -17,7 +17,8 @@ import pytest
 import torch
 
 from nanoserve_amd import paged_attention_hip
-from nanoserve_amd.attention import _workspaces, prepare_decode_plan
+from nanoserve_amd.attention import _attention, _workspaces, prepare_decode_plan
+from nanoserve_amd.capture import graph_capture
 from nanoserve_amd.workloads import make_case, metadata_for
 from oracle.paged_attention import dense_reference, paged_attention_ref
 from tests._helpers import build_paged, make_md, md_to
@@ -153,8 +154,9 @@ def test_decode_wider_table_and_larger_max_seq_len():
 
 
 def test_decode_prepared_plan_and_per_call_plan_agree_bitwise():
-    """The decode plan is built on the device from seq_lens, once per step
-    (prepare_decode_plan) or by each call; with or without the host copies of
+    """The decode plan is built on the device from seq_lens: by the step's first
+    call and stored on md, explicitly before it (prepare_decode_plan), or by the
+    library inside a call that shares none; with or without the host copies of
     the lengths the same plan, arithmetic and merge order give identical bits."""
     seqs = [5, 300, 4000, 77, 1, 2048, 0]
     q, kc, vc, md, tables, _ = _case(seqs, [1] * len(seqs), 14, 2, 64, 16, torch.float16)
@@ -165,8 +167,32 @@ def test_decode_prepared_plan_and_per_call_plan_agree_bitwise():
     prepare_decode_plan(mdd, kc.to(DEV))
     assert mdd.decode_plan is not None
     c = paged_attention_hip(q.to(DEV), kc.to(DEV), vc.to(DEV), mdd, 0.125).float().cpu()
-    assert torch.equal(a, b) and torch.equal(a, c)
+    own = md_to(md, DEV)
+    d = _attention(q.to(DEV), kc.to(DEV), vc.to(DEV), own, 0.125, share_plan=False).float().cpu()
+    assert own.decode_plan is None  # the library planned inside the call
+    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(a, d)
     _assert_close(a, paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
+
+
+def test_first_call_of_a_step_builds_the_plan_the_others_reuse():
+    """The unchanged reference call pattern (qwen2.py:59-65: one md, one call
+    per layer, no per-step hook): the first call stores the plan on md, later
+    calls reuse that same buffer, and a new md (the next step) gets its own."""
+    seqs = [700, 33, 1900, 260]
+    q, kc, vc, md, tables, _ = _case(seqs, [1] * 4, 14, 2, 64, 16, torch.float16)
+    mdd = md_to(md, DEV)
+    assert mdd.decode_plan is None
+    first = paged_attention_hip(q.to(DEV), kc.to(DEV), vc.to(DEV), mdd, 0.125)
+    plan = mdd.decode_plan
+    assert plan is not None
+    again = paged_attention_hip(q.to(DEV), kc.to(DEV), vc.to(DEV), mdd, 0.125)
+    assert mdd.decode_plan is plan
+    nxt = md_to(md, DEV)
+    paged_attention_hip(q.to(DEV), kc.to(DEV), vc.to(DEV), nxt, 0.125)
+    assert nxt.decode_plan is not None and nxt.decode_plan is not plan
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    _assert_close(first.float().cpu(), paged_attention_ref(q, kc, vc, md, 0.125), torch.float16)
 
 
 def test_decode_plan_is_shared_by_the_layers_of_a_step():
@@ -183,7 +209,7 @@ def test_decode_plan_is_shared_by_the_layers_of_a_step():
         kl = torch.randn(kc.shape, generator=g).half().to(DEV)
         vl = torch.randn(vc.shape, generator=g).half().to(DEV)
         shared = paged_attention_hip(ql, kl, vl, mdd, 0.125)
-        own = paged_attention_hip(ql, kl, vl, md_to(md, DEV), 0.125)
+        own = _attention(ql, kl, vl, md_to(md, DEV), 0.125, share_plan=False)
         torch.cuda.synchronize()
         assert torch.equal(shared, own), f"layer {layer}"
     # A plan for another head size does not apply to this call: it plans for itself.
@@ -408,7 +434,7 @@ def test_graph_replays_match_eager(config):
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=s):
+    with graph_capture(graph, stream=s):
         out = paged_attention_hip(case.query, case.k_cache, case.v_cache, case.md, case.scale)
     with torch.inference_mode():
         for _ in range(4):
