@@ -40,11 +40,27 @@ class SamplingParams:
     ignore_eos: bool = False
 
 
+PREEMPTION_MODES = ("recompute", "none")
+
+
 @dataclass
 class SchedulerConfig:
+    """Step budget, sequence cap, prompt chunking and what happens when the
+    cache runs out of blocks (reference config.py:68-83).
+
+    preemption_mode "recompute" evicts as rule 2 of the module docstring says;
+    "none" evicts nobody, so a grant the cache cannot hold stops the engine
+    with a RuntimeError (the reference's ablation, scheduler.py:213-243).
+    """
+
     max_num_batched_tokens: int = 2048
     max_num_seqs: int = 64
     enable_chunked_prefill: bool = True
+    preemption_mode: str = "recompute"
+
+    def __post_init__(self) -> None:
+        if self.preemption_mode not in PREEMPTION_MODES:
+            raise ValueError(f"preemption_mode must be one of {PREEMPTION_MODES}, got {self.preemption_mode!r}")
 
 
 class SeqState(enum.Enum):
@@ -239,9 +255,10 @@ class Scheduler:
     def _reserve_blocks(self, seq: Sequence, upto: int, admitted_order: list[Sequence], granted: set[int],
                         step: SchedulerOutput) -> bool:
         """Blocks for positions [0, upto) of `seq`, evicting newer sequences as needed."""
+        evicting = self.cfg.preemption_mode == "recompute"
         while not self.blocks.allocate(seq, upto):
             victim = None
-            for cand in reversed(admitted_order):
+            for cand in reversed(admitted_order) if evicting else ():
                 if cand is not seq and cand.state is SeqState.RUNNING and cand.seq_id not in granted:
                     victim = cand
                     break
@@ -251,6 +268,11 @@ class Scheduler:
                 if needed > usable:
                     raise ValueError(f"request {seq.seq_id} cannot fit the KV cache: {upto} tokens need "
                                      f"{needed} blocks of {self.blocks.block_size}, {usable} are usable")
+                if not evicting:
+                    raise RuntimeError(
+                        f"KV cache exhausted with preemption_mode='none': sequence {seq.seq_id} needs blocks "
+                        f"up to token {upto}, and the {len(self.running)} running sequences hold all "
+                        f"{self.blocks.num_total_blocks} blocks")
                 self._evict(seq, step)
                 return False
             self._evict(victim, step)

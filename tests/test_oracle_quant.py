@@ -129,3 +129,69 @@ def test_rope_pair_row_order(heads, D):
         for r in range(8):
             assert tile[r + 8] - tile[r] == D // 2 and tile[r] % D < D // 2
     assert rope_pair_order(heads, D).tolist() == order
+
+
+# quantize_model: the reference's model-level checks (tests/test_quant.py:120-166)
+# on the CPU; the conversion is setup-time tensor code and runs no kernel.
+
+def test_quantize_model_reports_real_compression():
+    from nanoserve_amd.quant import Int4Linear, quantize_model
+
+    m = torch.nn.Sequential(torch.nn.Linear(256, 256, bias=False), torch.nn.SiLU(),
+                            torch.nn.Linear(256, 256, bias=False))
+    report = quantize_model(m, 128, skip=())
+    assert report["mode"] == "int4" and report["group_size"] == 128
+    assert report["layers_quantized"] == 2
+    assert isinstance(m[0], Int4Linear) and isinstance(m[2], Int4Linear)
+    # 2 x 256 x 256 fp32 = 512 KiB before; after, per layer 256 x 128 code bytes
+    # + 256 x 2 scales (4 B) + 256 x 2 zero points (1 B) = 35,328 B.
+    assert report["weight_mib_before"] * 2**20 == 2 * 256 * 256 * 4
+    assert report["weight_mib_after"] * 2**20 == 2 * (256 * 128 + 256 * 2 * 4 + 256 * 2)
+    assert report["compression"] == pytest.approx(524288 / 70656)
+    assert report["freed_mib"] == pytest.approx(report["weight_mib_before"] - report["weight_mib_after"])
+
+
+def test_quantize_model_honours_skip_and_shape():
+    from nanoserve_amd.quant import Int4Linear, quantize_model
+
+    m = torch.nn.Sequential()
+    m.add_module("keep_me", torch.nn.Linear(128, 128, bias=False))
+    m.add_module("other", torch.nn.Linear(128, 128, bias=True))
+    inner = torch.nn.Sequential()
+    inner.add_module("deep", torch.nn.Linear(128, 64))
+    m.add_module("keep_me_too", inner)                  # a skipped subtree stays whole
+    m.add_module("ragged_in", torch.nn.Linear(100, 128))  # not a whole number of groups
+    m.add_module("ragged_out", torch.nn.Linear(128, 40))  # not a whole number of 16-row tiles
+    report = quantize_model(m, 128, skip=("keep_me",))
+    assert report["layers_quantized"] == 1
+    assert isinstance(m.other, Int4Linear) and m.other.bias is not None
+    for name in ("keep_me", "ragged_in", "ragged_out"):
+        assert type(getattr(m, name)) is torch.nn.Linear
+    assert type(m.keep_me_too.deep) is torch.nn.Linear
+
+
+def test_quantize_model_counts_tied_weights_once():
+    from nanoserve_amd.quant import quantize_model
+
+    a = torch.nn.Linear(64, 64, bias=False)
+    b = torch.nn.Linear(64, 64, bias=False)
+    b.weight = a.weight
+    m = torch.nn.Sequential(a, b)
+    report = quantize_model(m, 64, skip=("0", "1"))
+    assert report["layers_quantized"] == 0
+    assert report["weight_mib_before"] * 2**20 == 64 * 64 * 4 == report["weight_mib_after"] * 2**20
+
+
+def test_quantized_modules_hold_the_quantiser_bytes():
+    from nanoserve_amd.quant import quantize_model
+
+    torch.manual_seed(3)
+    m = torch.nn.Sequential(torch.nn.Linear(256, 128))
+    w = m[0].weight.detach().numpy().copy()
+    bias = m[0].bias.detach().clone()
+    quantize_model(m, 128, skip=())
+    rp, rs, rz = quantize_int4_ref(w, 128)
+    assert np.array_equal(m[0].qweight.numpy(), rp)
+    assert np.array_equal(m[0].scales.numpy(), rs)
+    assert np.array_equal(m[0].zeros.numpy(), rz)
+    assert torch.equal(m[0].bias.data, bias)

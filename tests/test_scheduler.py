@@ -18,9 +18,10 @@ from nanoserve_amd.block_manager import BlockSpaceManager
 from nanoserve_amd.scheduling import SamplingParams, Scheduler, SchedulerConfig, Sequence, SeqState
 
 
-def make(blocks=64, bs=16, budget=1024, max_seqs=256, chunked=True):
+def make(blocks=64, bs=16, budget=1024, max_seqs=256, chunked=True, preemption="recompute"):
     bm = BlockSpaceManager(bs, blocks, watermark=0.0)
-    cfg = SchedulerConfig(max_num_batched_tokens=budget, max_num_seqs=max_seqs, enable_chunked_prefill=chunked)
+    cfg = SchedulerConfig(max_num_batched_tokens=budget, max_num_seqs=max_seqs, enable_chunked_prefill=chunked,
+                          preemption_mode=preemption)
     return Scheduler(cfg, bm), bm
 
 
@@ -202,6 +203,42 @@ def test_an_evicted_request_goes_to_the_front_of_the_queue():
             break
         step(s, out)
     assert out.preempted and s.waiting[0] is out.preempted[0] and newcomer in s.waiting
+
+
+def test_without_preemption_exhaustion_raises_instead_of_evicting():
+    # The reference's ablation (scheduler.py:213-243): the case that evicts
+    # sequence 1 under "recompute" stops the engine under "none", and nothing
+    # was evicted before the error.
+    s, bm = make(budget=64, blocks=6, bs=4, preemption="none")
+    a, b = req(0, 11, max_new=8), req(1, 11, max_new=8)
+    s.add(a)
+    s.add(b)
+    step(s, s.schedule())
+    step(s, s.schedule())
+    with pytest.raises(RuntimeError, match="preemption_mode='none'"):
+        s.schedule()
+    assert s.num_preemptions == 0 and b.state is SeqState.RUNNING and len(b.block_table) == 3
+
+
+def test_without_preemption_a_fitting_workload_still_completes():
+    s, bm = make(blocks=64, budget=256, preemption="none")
+    for i in range(6):
+        s.add(req(i, 40, max_new=12))
+    done = drain(s)
+    assert len(done) == 6 and s.num_preemptions == 0 and bm.num_free_blocks == 64
+
+
+def test_without_preemption_an_oversized_request_is_still_a_value_error():
+    s, _ = make(blocks=2, budget=10_000, preemption="none")
+    s.add(req(0, 16, max_new=200))
+    with pytest.raises(ValueError, match="cannot fit the KV cache"):
+        drain(s, limit=400)
+
+
+def test_unknown_preemption_modes_are_rejected():
+    with pytest.raises(ValueError, match="preemption_mode"):
+        SchedulerConfig(preemption_mode="swap")
+    assert SchedulerConfig().preemption_mode == "recompute"
 
 
 def test_a_request_larger_than_the_cache_is_rejected():
