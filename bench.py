@@ -251,10 +251,17 @@ def _floors(torch, args):
     """What any kernel pays on this device, graph-replayed back to back: an empty
     launch, and one streaming read of N bytes from HBM (each launch reads its own
     slice of a pool larger than the 256 MB MALL), for c2's byte counts and a
-    large read.  ns_stream_read (csrc/floors.hip) is the kernel for both."""
-    from nanoserve_amd import _lib
+    large read.  ns_stream_read (csrc/floors.hip, a library of its own that only
+    this mode loads) is the kernel for both."""
+    import ctypes
 
-    lib = _lib.load()
+    from nanoserve_amd import _build, _lib
+
+    if not _build.FLOORS_LIB_PATH.exists():
+        raise FileNotFoundError(f"{_build.FLOORS_LIB_PATH} is not built (python -m nanoserve_amd._build)")
+    lib = ctypes.CDLL(str(_build.FLOORS_LIB_PATH))
+    lib.ns_stream_read.restype = ctypes.c_int
+    lib.ns_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     stream = torch.cuda.Stream()
     sink = torch.zeros(65536, dtype=torch.int32, device="cuda")
     pool_bytes = int(args.replica_gb * 1e9) // 4096 * 4096

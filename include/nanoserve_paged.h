@@ -248,16 +248,6 @@ int ns_argmax_rows(int64_t* out, const void* x, int64_t x_stride_row, int64_t M,
                    int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * ns_stream_read -- measurement floor, no counterpart in the reference: read
- * `bytes` (a multiple of 16, src 16-byte aligned) with 16-byte loads over
- * `grid` workgroups of 256 threads, each writing the XOR of what it read to
- * out[workgroup] (grid 32-bit words).  With bytes == 0 the launch does no
- * reads: the cost of an empty launch.  The benchmark's floors mode times it
- * next to the attention kernels.
- */
-int ns_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void* stream);
-
-/*
  * ns_paged_attention_workspace_size -- bytes of device workspace that
  * ns_paged_attention needs for these sizes: arrival counters, a region for
  * the call's own decode plan, the decode split-K slots and, without

@@ -102,9 +102,6 @@ SIGNATURES = {
         c_int64, c_int64, c_int,                 # M, N, dtype
         c_void_p, c_size_t, c_void_p,            # workspace, bytes, stream
     ]),
-    "ns_stream_read": (c_int, [
-        c_void_p, c_int64, c_void_p, c_int, c_void_p,  # src, bytes, out (u32 per workgroup), grid, stream
-    ]),
     "ns_paged_attention_workspace_size": (c_size_t, [
         c_int, c_int, c_int, c_int, c_int, c_int, c_int, c_int64, c_int,
     ]),

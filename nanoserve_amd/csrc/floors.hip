@@ -1,12 +1,16 @@
 // Measurement floors for the benchmark: what an empty launch and a plain
 // streaming read of N bytes cost on this device, so the attention kernels'
 // times can be put next to the best any kernel reading the same bytes does.
+// Built into a library of its own (libnanoserve_floors.so) that only the
+// benchmark loads; the product library and its header do not carry it.
 //
 // ns_stream_read reads `bytes` (a multiple of 16) from `src` with 16-byte
 // loads, each workgroup folding what it read into one 32-bit value written to
 // out[blockIdx.x] (so the loads cannot be dropped).  bytes == 0 launches
 // `grid` workgroups that only write their zero: the launch floor.
 #include "ns_common.h"
+
+extern "C" int ns_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void* stream);
 
 namespace ns {
 namespace {

@@ -36,6 +36,15 @@ def test_library_exports_every_declared_symbol():
     assert set(_declared_functions()) == set(_lib.SIGNATURES)
 
 
+def test_the_benchmark_probe_lives_outside_the_product_library():
+    from nanoserve_amd import _build
+
+    assert not hasattr(ctypes.CDLL(str(_lib.LIB_PATH)), "ns_stream_read")
+    if not _build.FLOORS_LIB_PATH.exists():
+        pytest.skip("the benchmark's probe library is not built")
+    assert hasattr(ctypes.CDLL(str(_build.FLOORS_LIB_PATH)), "ns_stream_read")
+
+
 def test_status_strings_and_version():
     lib = _lib.load()
     assert lib.ns_version() >= 100
