@@ -789,20 +789,6 @@ __global__ __launch_bounds__(W * 64) void paged_decode_kernel(AttnParams p) {
     if (idx < n_items) load_item(p, idx, r0, r1, ib);
     __syncthreads();  // the next item reuses the LDS
   }
-  // The next call of a step (every layer uses the step's plan) starts this
-  // workgroup index on the same XCD (blockIdx mod 8), reading the same first
-  // item and the header: read them once more now, with vector loads, so they
-  // sit in this XCD's L2 (c2 12.23 -> 12.15 us per call, c1 8.17 -> 8.09).
-  // Read-only and inside the plan buffer (the grid never exceeds its
-  // capacity).
-  if (threadIdx.x < 11) {
-    const u32x4* rows = reinterpret_cast<const u32x4*>(p.items + blockIdx.x);
-    const void* ptr = threadIdx.x < 10 ? static_cast<const void*>(rows + threadIdx.x)
-                                       : static_cast<const void*>(p.plan_hdr);
-    u32x4 v;
-    asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(ptr) : "memory");
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
 }
 
 // --------------------------------------------------------------------------
@@ -1354,24 +1340,7 @@ __global__ __launch_bounds__(kPrefillThreads) void paged_prefill_kernel(PrefillP
     if (tid == 0) __hip_atomic_store(&p.pf_counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
-  if (kg != 0 || !wave_on) {
-    // While group 0 stores the outputs, one wave of group 1 reads the
-    // workgroup's block-table entries once more: the next call of the step
-    // (every layer shares the step's tables) starts this workgroup index on
-    // the same XCD and finds its table window in that XCD's L2 (c3 43.95 ->
-    // 43.73 us).  Read-only, the entries the window loads above read.
-    if (kg == 1 && wc == 0) {
-      const int e_end = (kv_end + bs_mask) >> bs_shift;
-      const int e_beg = (M_begin * MKEYS) >> bs_shift;
-      for (int e = e_beg + lane; e < e_end; e += 64) {
-        const char* a = static_cast<const char*>(p.bt) + (bt_row + e) * static_cast<int64_t>(sizeof(BTI));
-        uint32_t v;
-        asm volatile("global_load_dword %0, %1, off" : "=v"(v) : "v"(a) : "memory");
-      }
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-    return;
-  }
+  if (kg != 0 || !wave_on) return;
 #pragma unroll
   for (int ct = 0; ct < CT; ++ct) {
     const float lsum = group4_sum_swap(l_run[ct]);
