@@ -70,6 +70,10 @@ struct Int4LinearParams {
   // gemm_splits K splits (split-K for the tiles of a last, part-filled
   // dispatch round, or for every tile when gemm_whole is 0).
   int gemm_gx, gemm_whole, gemm_splits;
+  // Group of a 32-k half n (n = 2 * step + half): n / gemm_gh with
+  // gemm_gh = group_size / 32, computed as umulhi(n, gemm_ghinv) (ceil(2^32 /
+  // gemm_gh); exact since n * gemm_gh < 2^32) or n itself when gemm_gh is 1.
+  uint32_t gemm_gh, gemm_ghinv;
 };
 
 // Device-scope (sc1) buffer accesses carry partials between workgroups, which
@@ -715,8 +719,9 @@ bool aligned(const void* q, uintptr_t a) { return reinterpret_cast<uintptr_t>(q)
 // dequantize_int4's arithmetic (quant.py:83-95) one step ahead of the MFMAs
 // that use them (software pipeline: step s+1's dequantisation and step s's
 // MFMAs are independent work in one block).  x rows in LDS are 128 bytes
-// with 16-byte unit c of row r at c ^ (r & 7), so the operand reads of a
-// wave spread over the banks.  Every wait for the ring is an explicit vmcnt
+// with 16-byte unit c of row r at c ^ ((r >> 1) & 7), and code rows swap
+// their 16-byte halves when bit 3 of the row is set, so the operand reads of
+// a wave meet every bank once.  Every wait for the ring is an explicit vmcnt
 // (the loads are issued from asm, invisible to the compiler's wait-count
 // pass).
 //
@@ -738,19 +743,21 @@ template <int BM, int BN, int NST, int WN>
 struct Cfg {
   static constexpr int X_B = BM * ROW_B;       // x tile of a stage
   static constexpr int C_B = BN * BK / 2;      // weight codes of a stage (32 bytes a row)
-  static constexpr int SZ_B = BN * 2 * 4;      // a scale (or zero-point word) per row and 32-k half
+  static constexpr int SZ_B = BN * 4;          // a scale (or zero-point word) per row
   static constexpr int STAGE_B = X_B + C_B + 2 * SZ_B;
   static constexpr int LDS = NST * STAGE_B;
   static constexpr int X_DMA = X_B / 1024 / WAVES;  // 16-byte global_load_lds per wave
-  // Per wave and step: x loads, one code load, one scale and one zero-point
-  // load (waves past the table's size repeat an earlier wave's loads, the
-  // same bytes to the same LDS words, so every wave counts the same).
-  static constexpr int PS = X_DMA + 3;
+  // Besides its x loads, each wave takes an equal share of the stage's other
+  // loads: the code loads (1 KiB each), then the scale loads and then the
+  // zero-point loads (64 rows each).  No load repeats another.
+  static constexpr int CODE_L = C_B / 1024, SZ_L = BN / 64;
+  static constexpr int EXTRA = (CODE_L + 2 * SZ_L) / WAVES;
+  static constexpr int PS = X_DMA + EXTRA;  // loads per wave and step
   static constexpr int WM = WAVES / WN;
   static constexpr int WF = BN / WN, WT = BM / WM;  // features and tokens of one wave
   static constexpr int FT = WF / 16, TT = WT / 16;  // 16-row MFMA tiles per wave: features, tokens
-  static_assert(X_B % (1024 * WAVES) == 0 && C_B % 1024 == 0 && SZ_B % 256 == 0, "whole loads per wave");
-  static_assert(C_B <= 1024 * WAVES && SZ_B <= 256 * WAVES, "one code, scale and zero load per lane cover a step");
+  static_assert(X_B % (1024 * WAVES) == 0 && C_B % 1024 == 0 && BN % 64 == 0, "whole loads per wave");
+  static_assert((CODE_L + 2 * SZ_L) % WAVES == 0, "the waves share the code, scale and zero loads evenly");
   static_assert(NST >= 3, "the loop dequantises one step ahead of its MFMAs");
   static_assert(LDS <= 80 * 1024, "two workgroups fit one CU's LDS");
 };
@@ -782,13 +789,19 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
   const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, c16 = lane & 15;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = w % WN, wm = w / WN;
-  // Grid: tile t = (token tile t / gx, feature tile t % gx), so consecutive
-  // workgroups share one x row block, spread over the XCDs by the round-robin
-  // dispatch (an XCD-local renumbering measured slower).  Workgroup b <
-  // gemm_whole takes tile b whole; the rest take split z of tile gemm_whole +
-  // st, workgroup gemm_whole + z * split_tiles + st, so one round of splits
-  // covers every split tile.
-  const int gx = p.gemm_gx, b = blockIdx.x;
+  // Grid: work unit b is tile t = (token tile t / gx, feature tile t % gx),
+  // so consecutive units share one x row block.  Unit b < gemm_whole takes
+  // tile b whole; the rest take split z of tile gemm_whole + st, unit
+  // gemm_whole + z * split_tiles + st, so one round of splits covers every
+  // split tile.  The dispatcher deals workgroup i to XCD i % 8; workgroup i
+  // takes unit b from a contiguous eighth of the units per XCD, so the
+  // workgroups of one XCD share x row blocks in that XCD's L2 (down_proj at
+  // 1024 tokens 34.4 -> 32.7 us, o_proj at 2048 14.7 -> 13.7 us on MI355X).
+  const int gx = p.gemm_gx;
+  const int b = [] {
+    const int units = gridDim.x, q = units >> 3, r = units & 7, xcd = blockIdx.x & 7;
+    return xcd * q + min(xcd, r) + static_cast<int>(blockIdx.x >> 3);
+  }();
   const int split_tiles = ((p.M + BM - 1) / BM) * gx - p.gemm_whole;
   int S = 1, z = 0, st = 0, tile = b;
   if (b >= p.gemm_whole) {
@@ -801,34 +814,69 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
   const int steps = p.K / BK;
   const int s0 = z * steps / S, s1 = (z + 1) * steps / S;
 
-  // Loader roles of this lane (rows past N repeat the last one, never stored).
-  const int cu = (w * 64 + lane) % (C::C_B / 16);  // 16-byte code unit: row cu/2, half cu&1
-  const int8_t* crow = reinterpret_cast<const int8_t*>(p.qweight) +
-                       static_cast<int64_t>(min(n0 + (cu >> 1), p.N - 1)) * (p.K / 2) + 16 * (cu & 1);
-  const int se = (w * 64 + lane) % (C::SZ_B / 4);  // scale entry: row se/2, 32-k half se&1
-  const int64_t sidx = static_cast<int64_t>(min(n0 + (se >> 1), p.N - 1)) * p.groups;
-  // This lane's operand rows: features WF wn + 16 fi + c16 of the tile.
-  int64_t zbase[FT];
+  // Loader roles of this lane (rows past M or N repeat the last one, never
+  // stored).  Each load is a uniform base, moved along K per step in scalar
+  // registers, plus a per-lane 32-bit byte offset fixed for the whole loop
+  // (the host takes this kernel only when every offset fits).  LDS layouts:
+  // 16-byte unit c of x row r sits at unit c ^ ((r >> 1) & 7) and the two
+  // 16-byte halves of code row r are swapped when bit 3 of r is set, so the
+  // operand reads of a wave (16 consecutive rows per quarter-wave) meet every
+  // bank once.
+  uint32_t xoff[C::X_DMA];
+#pragma unroll
+  for (int u = 0; u < C::X_DMA; ++u) {
+    const int unit = (w * C::X_DMA + u) * 64 + lane;
+    const int row = unit >> 3, pos = unit & 7;
+    const int m = min(m0 + row, p.M - 1);
+    xoff[u] = static_cast<uint32_t>((static_cast<int64_t>(m) * p.x_stride + 8 * (pos ^ ((row >> 1) & 7))) * ESZ);
+  }
+  // This wave's other loads: load e = w * EXTRA + j is code load e (16-byte
+  // unit 64e + lane: row u / 2, LDS half u & 1), or scale / zero-point load
+  // e - CODE_L (- SZ_L) of row 64 (e - ...) + lane.  The per-lane part of each
+  // address is fixed over the loop.
+  int ekind[C::EXTRA];  // 0 code, 1 scale, 2 zero point (uniform)
+  uint32_t eoff[C::EXTRA], edst[C::EXTRA];
+#pragma unroll
+  for (int j = 0; j < C::EXTRA; ++j) {
+    const int e = w * C::EXTRA + j;
+    if (e < C::CODE_L) {
+      const int cu = e * 64 + lane;
+      ekind[j] = 0;
+      eoff[j] = static_cast<uint32_t>(min(n0 + (cu >> 1), p.N - 1)) * static_cast<uint32_t>(p.K / 2) +
+                16u * ((cu & 1) ^ ((cu >> 4) & 1));
+      edst[j] = e * 1024;
+    } else {
+      const int k = e - C::CODE_L, kind = k < C::SZ_L ? 1 : 2, r = (k % C::SZ_L) * 64;
+      ekind[j] = kind;
+      eoff[j] = static_cast<uint32_t>(min(n0 + r + lane, p.N - 1)) * static_cast<uint32_t>(p.groups) *
+                (kind == 1 ? 4u : 1u);
+      edst[j] = r * 4;
+    }
+  }
+  // This lane's operand rows: features WF wn + 16 fi + c16 of the tile; the
+  // zero-point byte of group gi sits at byte (zrow + gi) & 3 of its word.
+  uint32_t zrow[FT];
 #pragma unroll
   for (int fi = 0; fi < FT; ++fi)
-    zbase[fi] = static_cast<int64_t>(min(n0 + C::WF * wn + 16 * fi + c16, p.N - 1)) * p.groups;
+    zrow[fi] = static_cast<uint32_t>(min(n0 + C::WF * wn + 16 * fi + c16, p.N - 1)) * static_cast<uint32_t>(p.groups);
+  auto group_of = [&](int n) -> int {
+    return p.gemm_gh == 1 ? n : static_cast<int>(__umulhi(static_cast<uint32_t>(n), p.gemm_ghinv));
+  };
 
   auto dma = [&](int s, int st) {
+    const char* xs = p.x + static_cast<int64_t>(BK * ESZ) * s;
 #pragma unroll
-    for (int u = 0; u < C::X_DMA; ++u) {
-      const int i = w * C::X_DMA + u;
-      const int unit = i * 64 + lane;
-      const int row = unit >> 3, pos = unit & 7;
-      const int m = min(m0 + row, p.M - 1);  // rows past M repeat the last one (never stored)
-      dma_lds16(p.x + (static_cast<int64_t>(m) * p.x_stride + BK * s + 8 * (pos ^ (row & 7))) * ESZ,
-                xst(st) + i * 1024);
+    for (int u = 0; u < C::X_DMA; ++u) dma_lds16_off(xs, xoff[u], xst(st) + (w * C::X_DMA + u) * 1024);
+    const uint32_t gi = static_cast<uint32_t>(group_of(2 * s));
+#pragma unroll
+    for (int j = 0; j < C::EXTRA; ++j) {
+      if (ekind[j] == 0)
+        dma_lds16_off(p.qweight + (BK / 2) * s, eoff[j], cst(st) + edst[j]);
+      else if (ekind[j] == 1)
+        dma_lds4_off(p.scales + gi, eoff[j], sst(st) + edst[j]);
+      else  // the aligned word holding the zero point (inside the table: N * groups is a multiple of 16)
+        dma_lds4_off(p.zeros, (eoff[j] + gi) & ~3u, zst(st) + edst[j]);
     }
-    dma_lds16(crow + (BK / 2) * s, cst(st) + (w * 1024) % C::C_B);
-    const int gi = (BK * s + 32 * (se & 1)) / p.group_size;
-    dma_lds4(p.scales + sidx + gi, sst(st) + (w * 256) % C::SZ_B);
-    // The aligned word holding the zero point (the table is 4-byte aligned and
-    // N * groups a multiple of 16, so the word lies inside it).
-    dma_lds4(p.zeros + ((sidx + gi) & ~int64_t{3}), zst(st) + (w * 256) % C::SZ_B);
   };
 
   floatx4 acc[FT][TT];
@@ -849,14 +897,15 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
   // k of the step in one group per lane, dequantised into both sub-steps.
   auto dequant_step = [&](int s, V8 (&a)[FT][2]) {
     const int st = stage(s);
-    const int gi = (BK * s + 16 * g) / p.group_size;
+    const uint32_t gi = static_cast<uint32_t>(group_of(2 * s));  // both halves of a step share a group
 #pragma unroll
     for (int fi = 0; fi < FT; ++fi) {
       const int r = C::WF * wn + 16 * fi + c16;
-      const u32x2 words = *reinterpret_cast<const u32x2*>(cst(st) + 32 * r + 8 * g);
-      const float scale = *reinterpret_cast<const float*>(sst(st) + 4 * (2 * r + (g >> 1)));
-      const uint32_t zword = *reinterpret_cast<const uint32_t*>(zst(st) + 4 * (2 * r + (g >> 1)));
-      const uint32_t zb = zero_bias_f16x2((zword >> (8 * ((zbase[fi] + gi) & 3))) & 0xFFu);
+      const u32x2 words =
+          *reinterpret_cast<const u32x2*>(cst(st) + 32 * r + 16 * ((g >> 1) ^ ((r >> 3) & 1)) + 8 * (g & 1));
+      const float scale = *reinterpret_cast<const float*>(sst(st) + 4 * r);
+      const uint32_t zword = *reinterpret_cast<const uint32_t*>(zst(st) + 4 * r);
+      const uint32_t zb = zero_bias_f16x2((zword >> (8 * ((zrow[fi] + gi) & 3u))) & 0xFFu);
       a[fi][0] = dequant8_mix<DT>(words[0], zb, scale, magic);
       a[fi][1] = dequant8_mix<DT>(words[1], zb, scale, magic);
     }
@@ -870,7 +919,7 @@ __global__ __launch_bounds__(gemm::THREADS, 2) void int4_gemm_kernel(Int4LinearP
 #pragma unroll
       for (int ti = 0; ti < TT; ++ti) {
         const int row = C::WT * wm + 16 * ti + c16;
-        const V8 b = *reinterpret_cast<const V8*>(xt + row * ROW_B + (((2 * g + j) ^ (c16 & 7)) << 4));
+        const V8 b = *reinterpret_cast<const V8*>(xt + row * ROW_B + (((2 * g + j) ^ ((row >> 1) & 7)) << 4));
 #pragma unroll
         for (int fi = 0; fi < FT; ++fi) acc[fi][ti] = mfma16x16x32(DT{}, a[fi][j], b, acc[fi][ti]);
       }
@@ -994,7 +1043,7 @@ struct GemmShape {
 constexpr int kGemmCUs = 256;
 constexpr int kLdsPerCU = 160 * 1024;
 constexpr int gemm_lds(int bm, int bn, int nst) {
-  return nst * (bm * gemm::ROW_B + bn * gemm::BK / 2 + 2 * bn * 2 * 4) + 16;
+  return nst * (bm * gemm::ROW_B + bn * gemm::BK / 2 + 2 * bn * 4) + 16;
 }
 
 // Tile shape and split count of a GEMM call, from measurements on MI355X
@@ -1159,8 +1208,13 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
   p.groups = K / group_size;
   // The GEMM has no RMSNorm prologue; its epilogue reads bias four at a time
   // and its loads take whole 4-byte words of the zero-point table.
-  const bool use_gemm = M > kGemmMinRows && !norm_weight && K % gemm::BK == 0 && (!bias || aligned(bias, 8)) &&
-                        aligned(zeros, 4);
+  // Its loads address x, the codes and the scales by 32-bit byte offsets.
+  const int64_t esz = 2, lim = int64_t{1} << 32;
+  const bool small = (M - 1) * x_stride_row * esz + int64_t{K} * esz < lim && int64_t{N} * (K / 2) < lim &&
+                     int64_t{N} * (K / group_size) * 4 < lim;
+  // A 64-wide K step of the GEMM lies inside one group.
+  const bool use_gemm = M > kGemmMinRows && !norm_weight && K % gemm::BK == 0 && group_size % gemm::BK == 0 &&
+                        (!bias || aligned(bias, 8)) && aligned(zeros, 4) && small;
   int splits = 1;
   if (splitk && (use_gemm || M <= kGemmMinRows)) {
     const SplitkLayout l = splitk_layout(M, N, K);
@@ -1182,6 +1236,8 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
     p.gemm_gx = (N + gs.bn - 1) / gs.bn;
     p.gemm_whole = static_cast<int>(gs.whole);
     p.gemm_splits = gs.splits;
+    p.gemm_gh = static_cast<uint32_t>(group_size / 32);
+    p.gemm_ghinv = p.gemm_gh == 1 ? 0u : static_cast<uint32_t>(((uint64_t{1} << 32) + p.gemm_gh - 1) / p.gemm_gh);
     e = dtype == NS_DTYPE_F16 ? launch_int4_gemm<F16>(p, gs, s) : launch_int4_gemm<BF16>(p, gs, s);
   } else
     e = dtype == NS_DTYPE_F16 ? launch_int4_linear<F16>(p, s, splits) : launch_int4_linear<BF16>(p, s, splits);

@@ -135,6 +135,21 @@ __device__ __forceinline__ void dma_lds16(const void* src, const void* lds) {
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(m) : "memory", "m0");
 }
+// The same with a uniform base address in an SGPR pair and a per-lane 32-bit
+// byte offset (the instruction's saddr form): no 64-bit address arithmetic
+// in the vector ALU.
+__device__ __forceinline__ void dma_lds16_off(const void* base, uint32_t off, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(m)
+               : "memory", "m0");
+}
+__device__ __forceinline__ void dma_lds4_off(const void* base, uint32_t off, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(m)
+               : "memory", "m0");
+}
 __device__ __forceinline__ void dma_lds4(const void* src, const void* lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane(
       static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(lds))));

@@ -43,12 +43,13 @@ def _check(got: torch.Tensor, ref: np.ndarray, dtype, what=""):
                            f"max err {np.abs(got - ref).max():.3e}")
 
 
-def _run(M, N, K, dtype, gs=128, bias=True, seed=0, x_scale=1.0):
+def _run(M, N, K, dtype, gs=128, bias=True, seed=0, x_scale=1.0, method="auto"):
     packed, s, z = _weights(N, K, gs, seed)
     g = torch.Generator().manual_seed(seed + 1)
     x = (torch.randn(M, K, generator=g) * x_scale).to(dtype)
     b = (torch.randn(N, generator=g) * 0.1).to(dtype) if bias else None
-    got = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), None if b is None else b.to(DEV), gs)
+    got = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), None if b is None else b.to(DEV), gs,
+                      method=method)
     torch.cuda.synchronize()
     w = dequantize_int4_ref(packed.numpy(), s.numpy(), z.numpy(), gs, NAME[dtype])
     ref = int4_linear_ref(x.float().numpy(), w, None if b is None else b.float().numpy())
@@ -249,10 +250,26 @@ def test_dequantize_is_bit_exact(dtype, N, K, gs):
 @pytest.mark.parametrize("M", [129, 700, 2048])
 def test_large_row_counts_take_the_tiled_gemm_within_one_rounding(M):
     """Every tile shape of the GEMM: 64 x 64 (all but the cases below), 128 tokens
-    x 64 features (K = 4864 at 2048 tokens), 128 x 128 (N = 4096 at 2048 tokens)."""
-    _run(M, 1152, 896, torch.float16, seed=M)
-    _run(M, 896, 4864, torch.bfloat16, seed=M + 1)
-    _run(M, 4096, 512, torch.bfloat16, seed=M + 2)
+    x 64 features (K = 4864 at 2048 tokens), 128 x 128 (N = 4096 at 2048 tokens).
+    method="fused" keeps the long-K layer on the tiled GEMM, which "auto" leaves
+    above 1024 tokens."""
+    _run(M, 1152, 896, torch.float16, seed=M, method="fused")
+    _run(M, 896, 4864, torch.bfloat16, seed=M + 1, method="fused")
+    _run(M, 4096, 512, torch.bfloat16, seed=M + 2, method="fused")
+
+
+@pytest.mark.parametrize("M,K,dequant", [(1024, 4864, False), (1025, 4864, True), (2048, 4864, True),
+                                         (2048, 896, False), (1100, 2048, True), (1100, 1920, False)])
+def test_auto_takes_the_faster_path_per_shape(M, K, dequant):
+    """"auto" runs the dequantise + library GEMM steps exactly when K >= LONG_K and
+    M > LONG_K_TILED_MAX_ROWS (its output is then bit-identical to method="dequant",
+    otherwise to "fused"), and either way stays within one rounding of the oracle."""
+    N = 896
+    got, x, (packed, s, z), b = _run(M, N, K, torch.float16, seed=M + K)
+    want = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), b.to(DEV), 128,
+                       method="dequant" if dequant else "fused")
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
 
 
 @pytest.mark.parametrize("gs", [32, 64, 256])
@@ -260,7 +277,8 @@ def test_large_row_counts_take_the_tiled_gemm_within_one_rounding(M):
 def test_tiled_gemm_group_sizes_and_partial_tiles(gs, M, N):
     """Token tiles past M (rows repeat the last one and are never stored), feature
     tiles past N (N = 1152 is nine 128-row tiles; 2048 sixteen), and group sizes
-    below and above the 64-wide K step."""
+    below (32: the fused kernel, as a 64-wide K step of the GEMM would span two
+    groups) and above the 64-wide K step."""
     _run(M, N, 768, torch.float16, gs=gs, seed=M + gs)
     _run(M, N, 512, torch.bfloat16, gs=gs, bias=False, seed=M + gs + 1)
 
