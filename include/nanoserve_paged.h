@@ -346,9 +346,12 @@ int ns_paged_decode_plan(void* plan, size_t plan_bytes,
  * query length differs has its reached outputs written as NaN (nothing is
  * read or written out of bounds).
  *
- * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches and out.
- * Supported: head_dim in {64, 128}; block_size a power of two;
- * num_heads / num_kv_heads <= 16.  Loops are bounded by each sequence's
+ * dtype is NS_DTYPE_F32, NS_DTYPE_F16 or NS_DTYPE_BF16 for query, caches
+ * and out.  The MFMA kernels take float16/bfloat16 with head_dim 64 or 128, a
+ * power-of-two block_size and num_heads / num_kv_heads <= 16 (all pointers
+ * 16-byte aligned); every other shape with head_dim <= 256 runs a generic
+ * float32-arithmetic kernel (pointers aligned to the element size) that
+ * reads no plan, workspace or aux stream.  Loops are bounded by each sequence's
  * length (never by the block-table width), so zero-padded table rows are
  * safe.  A block id outside [0, num_blocks) is never dereferenced; the
  * affected (sequence, head) outputs are written as NaN.

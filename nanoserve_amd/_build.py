@@ -23,7 +23,7 @@ INCLUDE = REPO_DIR / "include"
 LIB_NAME = "libnanoserve_paged.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 SOURCES = ["paged_attention.hip", "decode_plan.hip", "reshape_and_cache.hip", "rope_cache.hip",
-           "int4_linear.hip", "argmax.hip"]
+           "int4_linear.hip", "argmax.hip", "generic_attention.hip"]
 # The benchmark's measurement probe (an empty launch and a plain streaming
 # read) is a library of its own: nothing in the product loads or declares it.
 FLOORS_SOURCES = ["floors.hip"]

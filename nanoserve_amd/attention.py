@@ -10,8 +10,11 @@ sequence with context length L and query length ql attends to keys
 Everything runs on the GPU through libnanoserve_paged.so: the decode rows of a
 batch are one kernel launch over a work plan built on the device, with
 split-K partials merged inside the launch; any other batch adds one launch of
-the variable-length MFMA kernel.  There is no torch or Triton fallback; a
-missing library or an unsupported shape raises.
+the variable-length MFMA kernel.  Those kernels take float16/bfloat16 at head
+sizes 64 and 128; float32, other head sizes (up to 256), block sizes that are
+not powers of two and more than 16 query heads per KV head run the library's
+generic one-wave-per-row kernel instead.  There is no torch or Triton
+fallback; a missing library or an unsupported shape raises.
 
 The plan belongs to the step, like the metadata: the reference builds one
 AttentionMetadata per step and hands the same object to every layer
@@ -244,8 +247,8 @@ def _attention(query, k_cache, v_cache, md: AttentionMetadata, scale: float, sha
         raise ValueError("query and caches must be on the same device")
     if query.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
         raise TypeError(f"query/cache dtypes differ: {query.dtype}, {k_cache.dtype}, {v_cache.dtype}")
-    if query.dtype not in (torch.float16, torch.bfloat16):
-        raise TypeError(f"paged_attention_hip supports float16/bfloat16, got {query.dtype}")
+    if query.dtype not in _lib.DTYPE_CODES:
+        raise TypeError(f"paged_attention_hip supports float32/float16/bfloat16, got {query.dtype}")
     if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
         raise ValueError("caches must be contiguous [num_blocks, block_size, num_kv_heads, head_dim]")
     if md.num_tokens != num_tokens:
@@ -298,13 +301,17 @@ def _attention(query, k_cache, v_cache, md: AttentionMetadata, scale: float, sha
             f"unsupported attention shape: Hq={num_heads} Hkv={num_kv_heads} D={head_dim} "
             f"block_size={block_size}")
     ws = _workspace(device, stream, nbytes)
-    aux = (None, None, None) if decode_only else _aux_stream(device, stream)
+    # Shapes outside the MFMA kernels run the library's generic kernel, which
+    # takes no plan and no second stream (the library decides the same way).
+    generic = (q.dtype == torch.float32 or head_dim not in (64, 128)
+               or block_size & (block_size - 1) != 0 or num_heads // num_kv_heads > 16)
+    aux = (None, None, None) if decode_only or generic else _aux_stream(device, stream)
     plan = None
     # A batch whose host offsets show no one-row sequence has no decode rows:
     # the library launches no decode kernel and needs no plan.
     has_decode_rows = decode_only or qsl_host is None or lens_host is None or any(
         b - a == 1 for a, b in zip(md.query_start_loc_cpu[:md.num_seqs], md.query_start_loc_cpu[1:md.num_seqs + 1]))
-    if share_plan and has_decode_rows:
+    if share_plan and has_decode_rows and not generic:
         # Reuse md's plan only in the context that built it: eagerly, or inside
         # the same graph capture (whose replays rebuild it).  Anywhere else
         # this call builds the step's plan anew; a replaced plan that a

@@ -24,6 +24,7 @@
 #include <vector>
 
 #include "decode_plan.h"
+#include "generic_attention.h"
 #include "ns_common.h"
 
 namespace ns {
@@ -1702,8 +1703,12 @@ extern "C" size_t ns_paged_attention_workspace_size(int num_seqs, int num_heads,
   (void)max_query_len;
   (void)num_tokens;
   if (num_seqs <= 0 || num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads ||
-      block_size <= 0 || max_seq_len < 0 || (head_dim != 64 && head_dim != 128))
+      block_size <= 0 || max_seq_len < 0 || head_dim <= 0)
     return 0;
+  // The generic kernel (float32, other head sizes or block sizes, wide
+  // groups) uses no workspace; a token size keeps the buffer non-empty.
+  if (ns::generic_attention_takes(0, head_dim, block_size, num_heads / num_kv_heads))
+    return head_dim <= ns::kGenericMaxHeadDim ? 256 : 0;
   const ns::DecodeShape d =
       ns::decode_shape(num_seqs, num_kv_heads, ns::round_up_ctx(max_seq_len, block_size), head_dim, ns::kPlanCUs);
   return ns::workspace_layout(num_heads / num_kv_heads, head_dim, d.item_cap, !is_decode_only).total;
@@ -1820,12 +1825,43 @@ int paged_attention_entry(void* out, const void* query, const void* k_cache, con
   if (!is_decode_only && static_cast<int64_t>(max_seq_len) + block_size > 0x7FFFFFFF) return NS_ERR_UNSUPPORTED;
   if (max_seq_len < 0 || max_query_len < 0) return NS_ERR_INVALID_ARG;
   if (!(scale == scale)) return NS_ERR_INVALID_ARG;
-  const int bs_shift = ilog2_exact(block_size);
-  if (bs_shift < 0) return NS_ERR_UNSUPPORTED;
-  if (head_dim != 64 && head_dim != 128) return NS_ERR_UNSUPPORTED;
-  if (dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
+  if (block_size <= 0 || head_dim <= 0) return NS_ERR_INVALID_ARG;
+  if (dtype != NS_DTYPE_F32 && dtype != NS_DTYPE_F16 && dtype != NS_DTYPE_BF16) return NS_ERR_UNSUPPORTED;
   const int group = num_heads / num_kv_heads;
-  if (group > 16) return NS_ERR_UNSUPPORTED;
+  if (generic_attention_takes(dtype == NS_DTYPE_F32, head_dim, block_size, group)) {
+    // Shapes outside the MFMA kernels: the generic kernel, which needs no
+    // workspace, plan or second stream (those arguments are not read).
+    if (head_dim > kGenericMaxHeadDim || num_heads > 65535 || num_tokens > 0x7FFFFFFF) return NS_ERR_UNSUPPORTED;
+    const size_t esz = dtype == NS_DTYPE_F32 ? 4 : 2;
+    for (const void* a : {static_cast<const void*>(out), query, k_cache, v_cache})
+      if (reinterpret_cast<uintptr_t>(a) % esz != 0) return NS_ERR_INVALID_ARG;
+    GenericAttnParams g{};
+    g.out = out;
+    g.query = query;
+    g.k_cache = k_cache;
+    g.v_cache = v_cache;
+    g.bt = block_tables;
+    g.bt_stride = block_table_stride;
+    g.seq_lens = seq_lens;
+    g.qsl = query_start_loc;
+    g.bt64 = block_tables_is_int64 ? 1 : 0;
+    g.sl64 = seq_lens_is_int64 ? 1 : 0;
+    g.qsl64 = query_start_loc_is_int64 ? 1 : 0;
+    g.decode_only = is_decode_only ? 1 : 0;
+    g.num_seqs = num_seqs;
+    g.num_heads = num_heads;
+    g.num_kv_heads = num_kv_heads;
+    g.head_dim = head_dim;
+    g.block_size = block_size;
+    g.num_tokens = num_tokens;
+    g.num_blocks = num_blocks;
+    const int64_t ctx = round_up_ctx(max_seq_len, block_size), table = block_table_width * block_size;
+    g.max_ctx = ctx < table ? ctx : table;
+    g.scale = scale;
+    return launch_generic_attention(g, dtype, static_cast<hipStream_t>(stream)) == hipSuccess ? NS_OK
+                                                                                             : NS_ERR_HIP;
+  }
+  const int bs_shift = ilog2_exact(block_size);
   if (num_seqs > 65535 || num_kv_heads > 65535) return NS_ERR_UNSUPPORTED;
   if (!aligned16(out) || !aligned16(query) || !aligned16(k_cache) || !aligned16(v_cache))
     return NS_ERR_INVALID_ARG;

@@ -68,10 +68,12 @@ def _attn_args(**over):
     (dict(decode_only=0, qsl=None), _lib.NS_ERR_INVALID_ARG),
     (dict(T=3), _lib.NS_ERR_INVALID_ARG),                 # decode-only needs T == S
     (dict(Hq=15), _lib.NS_ERR_INVALID_ARG),               # Hq not a multiple of Hkv
-    (dict(D=96), _lib.NS_ERR_UNSUPPORTED),
-    (dict(bs=24), _lib.NS_ERR_UNSUPPORTED),               # not a power of two
-    (dict(dtype=_lib.NS_DTYPE_F32), _lib.NS_ERR_UNSUPPORTED),
-    (dict(Hq=64, Hkv=2), _lib.NS_ERR_UNSUPPORTED),        # 32 query heads per kv head
+    (dict(D=320), _lib.NS_ERR_UNSUPPORTED),               # beyond the generic kernel's 256
+    (dict(D=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(bs=0), _lib.NS_ERR_INVALID_ARG),
+    (dict(dtype=7), _lib.NS_ERR_UNSUPPORTED),              # no such dtype code
+    (dict(dtype=_lib.NS_DTYPE_F32, out=18), _lib.NS_ERR_INVALID_ARG),  # float32 rows misaligned
+    (dict(D=96, query=17), _lib.NS_ERR_INVALID_ARG),       # generic path: fp16 element misaligned
     (dict(ws=None), _lib.NS_ERR_WORKSPACE),
     (dict(ws_bytes=8), _lib.NS_ERR_WORKSPACE),
     (dict(bt_stride=2), _lib.NS_ERR_INVALID_ARG),         # stride below width
@@ -93,13 +95,22 @@ def test_empty_batch_is_a_no_op():
     assert lib.ns_paged_attention(*_attn_args(S=0, T=0, out=None)) == _lib.NS_OK
 
 
+def test_generic_shapes_need_only_a_token_workspace():
+    """float32, head sizes other than 64/128, non-power-of-two blocks and wide groups run the
+    generic kernel, which reads no workspace; head sizes past 256 are refused."""
+    lib = _lib.load()
+    for Hq, Hkv, D, bs in ((14, 2, 96, 16), (14, 2, 64, 24), (64, 2, 64, 16), (4, 2, 8, 4)):
+        assert lib.ns_paged_attention_workspace_size(8, Hq, Hkv, D, bs, 512, 1, 8, 1) == 256
+    assert lib.ns_paged_attention_workspace_size(8, 14, 2, 320, 16, 512, 1, 8, 1) == 0
+
+
 def test_workspace_size_is_monotone_in_context():
     lib = _lib.load()
     sizes = [lib.ns_paged_attention_workspace_size(32, 14, 2, 64, 16, L, 1, 32, 1)
              for L in (16, 256, 1024, 8192, 65536)]
     assert all(s > 0 for s in sizes)
     assert sizes == sorted(sizes)
-    assert lib.ns_paged_attention_workspace_size(32, 14, 2, 96, 16, 100, 1, 32, 1) == 0
+    assert lib.ns_paged_attention_workspace_size(32, 14, 2, 0, 16, 100, 1, 32, 1) == 0
 
 
 def _rc_args(**over):
