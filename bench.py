@@ -212,8 +212,9 @@ def _graph_time(torch, stream, launch, n, reps=3):
 def _int4_gemm(torch, args):
     """int4_linear at prefill token counts on the Qwen2.5-0.5B projections (fp16
     activations, INT4 g128 weights, each projection with the epilogue the model
-    gives it), graph-replayed: as Int4Linear calls it (method "auto", the figure
-    the line reports), the tiled GEMM alone ("fused"), and the reference's
+    gives it), graph-replayed: as Int4Linear calls it inside a captured graph
+    (method "auto", the figure the line reports), the tiled GEMM alone
+    ("fused", what "auto" runs eagerly), and the reference's
     QuantLinear steps (dequantize_int4 then F.linear, then the epilogue as tensor
     ops) on the same operands.  The HIP calls run with a split-K workspace, as
     Int4Linear does."""
@@ -232,7 +233,9 @@ def _int4_gemm(torch, args):
             bias = (torch.randn(N, generator=gen) * 0.1).half().to("cuda") if epi == "bias" else None
             res = torch.randn(M, N, generator=gen).half().to("cuda") if epi == "residual" else None
             t = {}
-            for method in ("auto", "fused", "dequant"):
+            # "dequant" first: its eager warm-up takes the weight scratch that
+            # "auto" may use inside a capture.
+            for method in ("dequant", "fused", "auto"):
                 def launch(i, method=method):
                     int4_linear(x, packed, scales, zeros, bias, 128, residual=res, silu_mul=epi == "silu_mul",
                                 method=method, workspace=ws if method != "dequant" else None)

@@ -261,15 +261,30 @@ def test_large_row_counts_take_the_tiled_gemm_within_one_rounding(M):
 @pytest.mark.parametrize("M,K,dequant", [(1024, 4864, False), (1025, 4864, True), (2048, 4864, True),
                                          (2048, 896, False), (1100, 2048, True), (1100, 1920, False)])
 def test_auto_takes_the_faster_path_per_shape(M, K, dequant):
-    """"auto" runs the dequantise + library GEMM steps exactly when K >= LONG_K and
-    M > LONG_K_TILED_MAX_ROWS (its output is then bit-identical to method="dequant",
-    otherwise to "fused"), and either way stays within one rounding of the oracle."""
+    """Eagerly "auto" is the tiled GEMM (bit-identical to method="fused"); recorded into a
+    graph it takes the dequantise + library GEMM steps exactly when K >= LONG_K and
+    M > LONG_K_TILED_MAX_ROWS (bit-identical to method="dequant"), and every replay stays
+    bit-identical with eager work between replays."""
+    from nanoserve_amd.capture import graph_capture
+
     N = 896
     got, x, (packed, s, z), b = _run(M, N, K, torch.float16, seed=M + K)
-    want = int4_linear(x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), b.to(DEV), 128,
-                       method="dequant" if dequant else "fused")
+    xd, pd, sd, zd, bd = x.to(DEV), packed.to(DEV), s.to(DEV), z.to(DEV), b.to(DEV)
+    fused = int4_linear(xd, pd, sd, zd, bd, 128, method="fused")
     torch.cuda.synchronize()
-    assert torch.equal(got, want)
+    assert torch.equal(got.to(DEV), fused)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        want = int4_linear(xd, pd, sd, zd, bd, 128, method="dequant" if dequant else "fused")  # takes the scratch
+    stream.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with graph_capture(g, stream=stream):
+        out = int4_linear(xd, pd, sd, zd, bd, 128)
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want)
+        fused.add_(0)  # eager work between replays
 
 
 @pytest.mark.parametrize("gs", [32, 64, 256])
