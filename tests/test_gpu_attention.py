@@ -465,15 +465,23 @@ def test_workspace_reused_across_shapes():
 
 
 def test_rejects_unsupported_shapes():
-    kc = torch.zeros(4, 16, 1, 96, device=DEV, dtype=torch.float16)
+    """Head sizes past 256 and non-float dtypes are refused; float32, head size 96 and 32
+    query heads per KV head run the generic kernel (tests/test_gpu_generic_attention.py)."""
     md = metadata_for([5], [1], [[0]], 16, DEV)
+    kc = torch.zeros(4, 16, 1, 320, device=DEV, dtype=torch.float16)
     with pytest.raises(RuntimeError):
-        paged_attention_hip(torch.zeros(1, 2, 96, device=DEV, dtype=torch.float16), kc, kc, md, 0.1)
-    kc = torch.zeros(4, 16, 1, 64, device=DEV, dtype=torch.float16)
-    with pytest.raises(RuntimeError):  # group of 32 heads per kv head
-        paged_attention_hip(torch.zeros(1, 32, 64, device=DEV, dtype=torch.float16), kc, kc, md, 0.1)
+        paged_attention_hip(torch.zeros(1, 2, 320, device=DEV, dtype=torch.float16), kc, kc, md, 0.1)
+    kc = torch.zeros(4, 16, 1, 64, device=DEV, dtype=torch.float64)
     with pytest.raises(TypeError):
-        paged_attention_hip(torch.zeros(1, 2, 64, device=DEV), kc.float(), kc.float(), md, 0.1)
+        paged_attention_hip(torch.zeros(1, 2, 64, device=DEV, dtype=torch.float64), kc, kc, md, 0.1)
+    kc = torch.zeros(4, 16, 1, 64, device=DEV, dtype=torch.float16)
+    with pytest.raises(TypeError):
+        paged_attention_hip(torch.zeros(1, 2, 64, device=DEV), kc, kc, md, 0.1)  # dtypes differ
+    for D, Hq, dtype in ((96, 2, torch.float16), (64, 32, torch.float16), (64, 2, torch.float32)):
+        kc = torch.zeros(4, 16, 1, D, device=DEV, dtype=dtype)
+        out = paged_attention_hip(torch.zeros(1, Hq, D, device=DEV, dtype=dtype), kc, kc, md, 0.1)
+        torch.cuda.synchronize()
+        assert out.shape == (1, Hq, D) and torch.count_nonzero(out) == 0  # zero values average to zero
 
 
 def test_workspace_counters_and_prefill_slots_are_left_zero():
