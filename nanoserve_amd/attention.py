@@ -204,6 +204,15 @@ def prepare_decode_plan(md: AttentionMetadata, cache: torch.Tensor) -> None:
     md.decode_plan = DecodePlan(buf, _plan_key(md, num_kv_heads, head_dim, block_size, device), capture)
 
 
+def takes_generic_kernel(dtype: torch.dtype, head_dim: int, block_size: int, group: int) -> bool:
+    """Whether the library runs this shape on its generic kernel (float32, head sizes
+    other than 64/128, block sizes that are not powers of two, more than 16 query heads
+    per KV head), which takes no decode plan and no second stream.  The library draws
+    the same line (generic_attention_takes in csrc/generic_attention.h)."""
+    return (dtype == torch.float32 or head_dim not in (64, 128)
+            or block_size & (block_size - 1) != 0 or group > 16)
+
+
 def workspace_bytes(md: AttentionMetadata, num_heads: int, num_kv_heads: int,
                     head_dim: int, block_size: int) -> int:
     """Device workspace ns_paged_attention needs for this metadata."""
@@ -301,10 +310,7 @@ def _attention(query, k_cache, v_cache, md: AttentionMetadata, scale: float, sha
             f"unsupported attention shape: Hq={num_heads} Hkv={num_kv_heads} D={head_dim} "
             f"block_size={block_size}")
     ws = _workspace(device, stream, nbytes)
-    # Shapes outside the MFMA kernels run the library's generic kernel, which
-    # takes no plan and no second stream (the library decides the same way).
-    generic = (q.dtype == torch.float32 or head_dim not in (64, 128)
-               or block_size & (block_size - 1) != 0 or num_heads // num_kv_heads > 16)
+    generic = takes_generic_kernel(q.dtype, head_dim, block_size, num_heads // num_kv_heads)
     aux = (None, None, None) if decode_only or generic else _aux_stream(device, stream)
     plan = None
     # A batch whose host offsets show no one-row sequence has no decode rows:

@@ -299,3 +299,20 @@ def test_argmax_workspace_size():
 ])
 def test_int4_dequantize_rejects_bad_arguments(args, code):
     assert _lib.load().ns_int4_dequantize(*args) == code
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,bs", [(14, 2, 64, 16), (28, 4, 128, 32), (14, 2, 96, 16), (4, 2, 8, 4),
+                                         (14, 2, 64, 12), (64, 2, 64, 16), (6, 3, 256, 1)])
+def test_the_shim_and_the_library_pick_the_same_kernel_family(Hq, Hkv, D, bs):
+    """attention.py skips the decode plan and the aux stream for the shapes the library
+    runs on its generic kernel; both must draw the line in the same place (the
+    library's workspace size is the token 256 bytes exactly for those shapes)."""
+    import torch
+
+    from nanoserve_amd.attention import takes_generic_kernel
+
+    lib = _lib.load()
+    generic_py = takes_generic_kernel(torch.float16, D, bs, Hq // Hkv)
+    assert takes_generic_kernel(torch.float32, D, bs, Hq // Hkv)
+    ws = lib.ns_paged_attention_workspace_size(8, Hq, Hkv, D, bs, 512, 1, 8, 1)
+    assert (ws == 256) == generic_py, (Hq, Hkv, D, bs, ws)
