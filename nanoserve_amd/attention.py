@@ -177,6 +177,8 @@ def prepare_decode_plan(md: AttentionMetadata, cache: torch.Tensor) -> None:
         return
     lib = _lib.load()
     _, block_size, num_kv_heads, head_dim = cache.shape
+    if takes_generic_kernel(cache.dtype, head_dim, block_size, 1):
+        return  # the generic kernel reads no plan
     device = cache.device
     bt = _index(md.block_tables, "block_tables", device)
     sl = _index(md.seq_lens, "seq_lens", device).contiguous()

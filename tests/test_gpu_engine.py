@@ -96,6 +96,32 @@ def test_forward_matches_oracle_on_a_mixed_batch(int4, fuse, dtype):
     assert relative_error(logits, want) < (TOL if dtype == torch.float16 else 3 * TOL)
 
 
+@pytest.mark.parametrize("cfg_kw,dtype,tol", [
+    (TINY, torch.float32, 1e-4),                                       # float32 model: the generic kernel
+    (dict(TINY, hidden_size=128, intermediate_size=256), torch.float16, TOL),  # head size 32
+])
+def test_forward_of_shapes_outside_the_mfma_kernels_matches_oracle(cfg_kw, dtype, tol):
+    """A float32 model and a head size of 32 run attention on the generic kernel (the
+    reference's model config takes any float dtype, config.py:15); the rest of the forward
+    (rotary + cache write, norms, unquantised projections) is unchanged.  Prefill of two
+    sequences, then one decodes while a third prefills."""
+    model = _model(cfg_kw, dtype=dtype, int4=False)
+    runner, bm = _runner(model)
+    a, b = _seq(0, _tokens(21, 512, 1)), _seq(1, _tokens(9, 512, 2))
+    kc = [t.cpu() for t in runner.kv_cache.k_cache]
+    vc = [t.cpu() for t in runner.kv_cache.v_cache]
+    logits, seqs, md, ids, pos = _step(runner, bm, [(a, 21), (b, 9)])
+    want, kc, vc = qwen2_forward_ref(model, ids, pos, kc, vc, md, torch.tensor([20, 29]))
+    torch.cuda.synchronize()
+    assert logits.dtype == dtype and relative_error(logits, want) < tol
+    a.output_token_ids.append(int(want[0].argmax()))
+    c = _seq(2, _tokens(30, 512, 3))
+    logits, seqs, md, ids, pos = _step(runner, bm, [(a, 1), (c, 30)])
+    want, _, _ = qwen2_forward_ref(model, ids, pos, kc, vc, md, torch.tensor([0, 30]))
+    torch.cuda.synchronize()
+    assert relative_error(logits, want) < tol
+
+
 def test_qwen_half_billion_shapes_two_layers_match_oracle():
     cfg = dict(num_hidden_layers=2)  # Qwen2.5-0.5B widths: hidden 896, 14/2 heads, D 64, vocab 151936
     model = _model(cfg, std=0.02)
