@@ -281,9 +281,11 @@ def test_decode_graph_replays_match_eager_steps(batch):
         toks = want.argmax(-1).tolist()
 
 
-def test_engine_with_graphs_completes_the_same_requests():
+@pytest.mark.parametrize("dtype,int4", [(torch.float16, True), (torch.float32, False)])
+def test_engine_with_graphs_completes_the_same_requests(dtype, int4):
+    """float32 (unquantised) runs attention on the generic kernel inside the graphs."""
     def run(graphs):
-        model = _model(seed=6)
+        model = _model(seed=6, dtype=dtype, int4=int4)
         eng = LLMEngine(model, num_blocks=128, block_size=8, device=DEV,
                         scheduler_config=SchedulerConfig(max_num_batched_tokens=64, max_num_seqs=8),
                         max_model_len=256, use_graphs=graphs)
