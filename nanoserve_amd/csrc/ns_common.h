@@ -181,13 +181,4 @@ __device__ __forceinline__ void lds_ready(V& x) {
   asm volatile("" : "+v"(x));
 }
 
-// LDS ordering between lanes of one wave: LDS instructions of a wave execute
-// in order, so a compiler-level fence is enough to make one lane's ds_write
-// visible to another lane's later ds_read.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 }  // namespace ns

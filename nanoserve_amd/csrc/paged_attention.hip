@@ -117,38 +117,39 @@ struct DecodeCfg {
   static constexpr int SLOT_B = 2 * TILE_B;
   static constexpr int QD = 16 * D * 2 / 1024;   // global_load_lds of the 16-row query tile
   static constexpr int Q_B = QD * 1024;
-  static constexpr int IDC_B = 64;               // the item's carried block ids (8 int32)
+  static constexpr int CARRIED = kItemBlocks / W;  // tiles per wave whose block ids come with the item
   static constexpr int IDS_B = 512;              // later block-table entries: 64 low words, 64 high words
-  static constexpr int WAVE_B = R * SLOT_B + Q_B + IDC_B + IDS_B;
+  static constexpr int WAVE_B = R * SLOT_B + Q_B + IDS_B;
   static constexpr int RED_LD = D + 4;           // padded row of a wave's block in the cross-wave reduce
   static constexpr int LDS = W * WAVE_B;
-  static_assert((R - 1) * PER_CHUNK <= 63, "waits fit vmcnt");
-  static_assert(2 * R <= kItemBlocks / W, "the first R chunks' tiles are carried by the item");
+  static_assert((R - 1) * PER_CHUNK + 2 <= 63, "waits (with two later table loads) fit vmcnt");
+  static_assert(2 * R <= CARRIED && CARRIED % 2 == 0 && CARRIED <= 8, "the first R chunks' tiles are carried by the item");
 };
 
-// Wait until at most k chunks (k * PC vector-memory operations) of this wave
-// are in flight; k is wave-uniform and below R.
-template <int PC, int R>
+// Wait until at most k chunks (k * PC vector-memory operations) of this wave,
+// plus X operations issued after them, are in flight; k is wave-uniform and
+// below R.
+template <int PC, int R, int X = 0>
 __device__ __forceinline__ void wait_chunks(int k) {
   if constexpr (R > 3) {
     if (k >= 3) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PC) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(3 * PC + X) : "memory");
       return;
     }
   }
   if constexpr (R > 2) {
     if (k >= 2) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PC) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PC + X) : "memory");
       return;
     }
   }
   if constexpr (R > 1) {
     if (k >= 1) {
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PC) : "memory");
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(PC + X) : "memory");
       return;
     }
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(X) : "memory");
 }
 
 // Split-K state crosses workgroups (and XCDs, whose L2s are not coherent
@@ -321,11 +322,10 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
   const T* kbase = reinterpret_cast<const T*>(p.k_cache) + static_cast<int64_t>(kvh) * D;
   const T* vbase = reinterpret_cast<const T*>(p.v_cache) + static_cast<int64_t>(kvh) * D;
 
-  // This wave's LDS: the chunk ring, the query tile, carried and later block ids.
+  // This wave's LDS: the chunk ring, the query tile, the block ids past the carried ones.
   char* ring = smem + w * Cfg::WAVE_B;
   char* qlds = ring + R * SLOT_B;
-  int32_t* idc = reinterpret_cast<int32_t*>(qlds + Cfg::Q_B);
-  char* ids = qlds + Cfg::Q_B + Cfg::IDC_B;
+  char* ids = qlds + Cfg::Q_B;
 
   int bad = 0;
   float m_run = -INFINITY, l_run = 0.f;
@@ -333,19 +333,24 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
 #pragma unroll
   for (int n = 0; n < NN; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Block id of the wave's tile `tile` for a chunk past the first R (BIG):
-  // the carried ones from idc, the later ones from the table entries the
-  // wave loaded into `ids`.  Uniform, so the DMA addresses stay scalar.
-  const int64_t e_first = (wb + 128) >> bs_shift;  // table entry of tile 8
+  // Block id of the wave's tile `tile` >= 8 (BIG), from the table entries
+  // the wave loaded into `ids`.  Uniform, so the DMA addresses stay scalar.
+  // Tiles 0-7 come with the item and stay in scalar registers (ib): reading
+  // them back from LDS would put an LDS read and its wait in front of every
+  // chunk's loads, which measured 0.18 us per call slower on c1 (8.08 against
+  // 7.90) and 0.08 us on c2.
+  const int64_t e_first = (wb + 16 * Cfg::CARRIED) >> bs_shift;  // table entry of the first tile not carried
+  auto carried_block = [&](int tile) -> int64_t {
+    int32_t v = ib.id[0];
+#pragma unroll
+    for (int j = 1; j < Cfg::CARRIED; ++j) v = tile == j ? ib.id[j] : v;
+    return v;
+  };
   auto tile_block = [&](int tile) -> int64_t {
     uint32_t lo, hi = 0;
-    if (tile < 8) {
-      lo = ds_read_b32(idc + tile);
-    } else {
-      const int64_t e = ((wb + 16 * static_cast<int64_t>(tile)) >> bs_shift) - e_first;
-      lo = ds_read_b32(ids + 4 * e);
-      if constexpr (sizeof(BTI) == 8) hi = ds_read_b32(ids + 256 + 4 * e);
-    }
+    const int64_t e = ((wb + 16 * static_cast<int64_t>(tile)) >> bs_shift) - e_first;
+    lo = ds_read_b32(ids + 4 * e);
+    if constexpr (sizeof(BTI) == 8) hi = ds_read_b32(ids + 256 + 4 * e);
     lds_wait_all();
     lds_ready(lo);
     lds_ready(hi);
@@ -576,19 +581,12 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
 
   if (nch > 0) {
     // The query tile (rows: the group's heads; rows past G repeat the last
-    // head and are zeroed when read), then, for waves with more than eight
-    // tiles, the table entries from tile 8 on: both land before chunk 0.
-    if constexpr (BIG) {
-      // Carried ids to LDS for chunks past the first R, before any DMA is
-      // in flight (one lane, two 16-byte stores).
-      if (nch > R && lane == 0) {
-        *reinterpret_cast<u32x4*>(idc) = u32x4{static_cast<uint32_t>(ib.id[0]), static_cast<uint32_t>(ib.id[1]),
-                                               static_cast<uint32_t>(ib.id[2]), static_cast<uint32_t>(ib.id[3])};
-        *reinterpret_cast<u32x4*>(idc + 4) = u32x4{static_cast<uint32_t>(ib.id[4]), static_cast<uint32_t>(ib.id[5]),
-                                                   static_cast<uint32_t>(ib.id[6]), static_cast<uint32_t>(ib.id[7])};
-      }
-      wave_lds_sync();
-    }
+    // head and are zeroed when read), then, for waves with more tiles than
+    // the item carries, the table entries from the first tile not carried
+    // on: both land before chunk 0.  Waves with only carried tiles skip the
+    // table load: issued by every wave, it delayed every wave's first data
+    // (c1 8.10 -> 7.84 us, c2 12.16 -> 12.01 us per call on MI355X without
+    // it).
     {
       const T* qg = reinterpret_cast<const T*>(p.query) + (qtok * p.num_heads + static_cast<int64_t>(kvh) * G) * D;
 #pragma unroll
@@ -600,11 +598,9 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
       }
     }
     if constexpr (BIG) {
-      {
+      if (wtiles > Cfg::CARRIED) {
         // Lane l: entry e_first + l (at most the wave's last), low words at
-        // ids[l], high words (int64 tables) at ids[64 + l].  Issued by every
-        // wave (a wave with eight tiles or fewer reads its last entry), so no
-        // branch separates these loads from the chunks'.
+        // ids[l], high words (int64 tables) at ids[64 + l].
         const int64_t e_last = (we - 1) >> bs_shift;
         int64_t e = e_first + lane;
         e = e <= e_last ? e : e_last;
@@ -660,8 +656,15 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
       if (nx < nch) {
         // The slot's LDS reads are done (their results were used above).
         if constexpr (BIG) {
-          const int64_t a = tile_block(2 * nx);
-          issue_chunk(nx, slot, a, 2 * nx + 1 < wtiles ? tile_block(2 * nx + 1) : a);
+          int64_t a, b;
+          if (2 * nx + 1 < Cfg::CARRIED) {
+            a = carried_block(2 * nx);
+            b = carried_block(2 * nx + 1);
+          } else {
+            a = tile_block(2 * nx);
+            b = 2 * nx + 1 < wtiles ? tile_block(2 * nx + 1) : a;
+          }
+          issue_chunk(nx, slot, a, 2 * nx + 1 < wtiles ? b : a);
         } else {
           issue_chunk(nx, slot, 0, 0);
         }
