@@ -177,11 +177,11 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
   // BATCH: 128-wide chunks whose weights one wave loads at once (1 when every
   // wave has a single chunk, which keeps the register count low).
   // FT: 16-feature row tiles per workgroup (several only with one chunk per wave).
-  // NORM: the RMSNorm prologue (p.norm_weight), in its own instantiation
-  // because its registers would lower every projection's occupancy (the
-  // 7-wave kernel needs 52 VGPRs without it, 83 with it).
+  // NORM: RMS-normalise the rows of x with p.norm_weight, in its own
+  // instantiation so that its registers do not lower every projection's
+  // occupancy.
   static_assert(FT == 1 || BATCH == 1, "feature tiles need one chunk per wave");
-  static_assert(!NORM || (BATCH == 1 && FT == 1), "the RMSNorm prologue runs one chunk and one tile per wave");
+  static_assert(!NORM || BATCH == 1, "the RMSNorm runs with one chunk per wave");
   // ROPE: the epilogue rotates q and k and writes q' to out, k' and v to their
   // cache slots (the steps between the q|k|v projection and attention).
   static_assert(!ROPE || (BATCH == 1 && FT == 1), "the rotary epilogue runs one tile per workgroup");
@@ -280,12 +280,19 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[f][t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
+  // NORM: rms_norm(x) = x * rstd(x) * w with rstd = rsqrt(mean(x^2) + eps)
+  // per row, so W·rms_norm(x) = rstd(x) * (W·(x * w)).  Each wave (one
+  // 128-wide chunk of K, the host guarantees) multiplies its x operands by
+  // the norm weight as they arrive, rounding x * w to the model dtype once,
+  // and adds up its slice of the rows' sums of squares in fp32; the sums meet
+  // in wave 0 with the partial products, which scales the accumulators by
+  // rstd before the epilogue.  No barrier stands between the loads and the
+  // MFMAs.  Against normalising first (torch's rms_norm rounds x * rstd * w
+  // once) an operand rounds at the same relative precision.
+  float ss[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) ss[t] = 0.f;
   if constexpr (NORM) {
-    // RMSNorm prologue (the host guarantees one 128-wide chunk per wave):
-    // every wave already holds its slice of each x row, so the rows' sums
-    // of squares meet in LDS and the operands are scaled in registers,
-    // y = round((x * rsqrt(mean(x^2) + eps)) * w) as torch's fused
-    // rms_norm evaluates it.
     const int kb = 128 * wave + 32 * grp;
     const int gi = kb / p.group_size;
     u32x4 codes[FT];
@@ -307,35 +314,16 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
       for (int t = 0; t < NT; ++t) b[j][t] = load16<DT>(xrow[t] + (kb + 8 * j) * ESZ);
     }
     __builtin_amdgcn_sched_barrier(0);
-    __shared__ float nss[WAVES][NT][16];
-    float ss[NT];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      ss[t] = 0.f;
+    for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float v = static_cast<float>(b[j][t][e]);
-          ss[t] += v * v;
+          ss[t] = __builtin_fmaf(v, v, ss[t]);
+          b[j][t][e] = to_model<DT>(v * static_cast<float>(nw[j][e]));
         }
-      ss[t] += __shfl_xor(ss[t], 16);  // the four lane groups holding this row
-      ss[t] += __shfl_xor(ss[t], 32);
-      if (grp == 0) nss[wave][t][row] = ss[t];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      float tot = 0.f;
-#pragma unroll
-      for (int w = 0; w < WAVES; ++w) tot += nss[w][t][row];
-      const float rstd = rsqrtf(tot / static_cast<float>(p.K) + p.norm_eps);
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          b[j][t][e] = to_model<DT>(static_cast<float>(b[j][t][e]) * rstd * static_cast<float>(nw[j][e]));
-    }
 #pragma unroll
     for (int f = 0; f < FT; ++f) {
       const float zero = static_cast<float>(zq[f]);
@@ -345,6 +333,11 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 #pragma unroll
         for (int t = 0; t < NT; ++t) acc[f][t] = mfma16x16x32(DT{}, a, b[j][t], acc[f][t]);
       }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      ss[t] += __shfl_xor(ss[t], 16);  // the four lane groups holding this row
+      ss[t] += __shfl_xor(ss[t], 32);
     }
   }
 
@@ -457,14 +450,22 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
   }
 
-  // Waves 1.. hand their partial sums to wave 0.
+  // Waves 1.. hand their partial sums (and, with NORM, their slices of the
+  // rows' sums of squares) to wave 0.
   if constexpr (WAVES > 1) {
     __shared__ floatx4 red[WAVES - 1][FT][NT][64];
+    __shared__ float nss[NORM ? WAVES - 1 : 1][NT][16];
     if (wave > 0) {
 #pragma unroll
       for (int f = 0; f < FT; ++f)
 #pragma unroll
         for (int t = 0; t < NT; ++t) red[wave - 1][f][t][lane] = acc[f][t];
+      if constexpr (NORM) {
+        if (grp == 0) {
+#pragma unroll
+          for (int t = 0; t < NT; ++t) nss[wave - 1][t][row] = ss[t];
+        }
+      }
     }
     __syncthreads();
     if (wave != 0) return;
@@ -475,6 +476,20 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
 #pragma unroll
         for (int w = 0; w < WAVES - 1; ++w) acc[f][t] += red[w][f][t][lane];
       }
+    if constexpr (NORM) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int w = 0; w < WAVES - 1; ++w) ss[t] += nss[w][t][row];
+    }
+  }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const float rstd = rsqrtf(ss[t] / static_cast<float>(p.K) + p.norm_eps);
+#pragma unroll
+      for (int f = 0; f < FT; ++f) acc[f][t] *= rstd;
+    }
   }
 
   if constexpr (BATCH > 1) {
@@ -611,11 +626,11 @@ struct Shape {
   int ft;
 };
 
-Shape shape_for(int M, int N, int K, int mt, int mtiles, bool norm) {
+Shape shape_for(int M, int N, int K, int mt, int mtiles) {
   const int chunks = K / 128;
   if (chunks >= 1 && chunks <= 8) {
     // (64-token tiles with two feature tiles would spill: 256 VGPRs.)
-    const bool two = !norm && mt == 16 && M >= 16 && N % 32 == 0 && static_cast<int64_t>(N / 32) * mtiles >= 256;
+    const bool two = mt == 16 && M >= 16 && N % 32 == 0 && static_cast<int64_t>(N / 32) * mtiles >= 256;
     return {chunks, 1, two ? 2 : 1};
   }
   if (K <= 2048) return {8, 4, 1};
@@ -639,11 +654,10 @@ const void* one_chunk_kernel(int waves) {
 template <class DT, int MT>
 const void* kernel_for(Shape sh, bool norm) {
   if (sh.batch == 1) {
-    if (norm) return one_chunk_kernel<DT, MT, 1, true>(sh.waves);
     if constexpr (MT == 16) {
-      if (sh.ft == 2) return one_chunk_kernel<DT, MT, 2, false>(sh.waves);
+      if (sh.ft == 2) return norm ? one_chunk_kernel<DT, MT, 2, true>(sh.waves) : one_chunk_kernel<DT, MT, 2, false>(sh.waves);
     }
-    return one_chunk_kernel<DT, MT, 1, false>(sh.waves);
+    return norm ? one_chunk_kernel<DT, MT, 1, true>(sh.waves) : one_chunk_kernel<DT, MT, 1, false>(sh.waves);
   }
   if constexpr (MT <= 16) {
     if (sh.waves == 16) return reinterpret_cast<const void*>(&int4_linear_kernel<DT, MT, 16, 4, 1, false, false>);
@@ -690,7 +704,7 @@ hipError_t launch_int4_linear(const Int4LinearParams& p, hipStream_t stream, int
   const int mt = p.M <= 64 ? 16 : 64;
   const int mtiles = (p.M + mt - 1) / mt;
   const bool norm = p.norm_weight != nullptr;
-  const Shape sh = shape_for(p.M, p.N, p.K, mt, mtiles, norm);
+  const Shape sh = shape_for(p.M, p.N, p.K, mt, mtiles);
   const void* fn = mt == 16 ? kernel_for<DT, 16>(sh, norm) : kernel_for<DT, 64>(sh, norm);
   const dim3 grid(static_cast<unsigned>(p.N / (16 * sh.ft)), static_cast<unsigned>(mtiles),
                   static_cast<unsigned>(sh.batch > 1 ? splits : 1));

@@ -236,6 +236,56 @@ def test_rmsnorm_prologue(dtype, K, M):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("M", [1, 16, 32, 64, 100])
+def test_rmsnorm_with_gate_up_silu_mul(dtype, M):
+    """Qwen2's MLP input: silu(gate(rms_norm(x))) * up(rms_norm(x)) in one launch, at
+    gate|up's width (4864 pairs), where 16-64 tokens take two feature tiles per
+    workgroup and 100 tokens a 64-token tile."""
+    K, I = 896, 4864
+    g = torch.Generator().manual_seed(31)
+    gate = torch.nn.Linear(K, I, bias=False).to(dtype)
+    up = torch.nn.Linear(K, I, bias=False).to(dtype)
+    with torch.no_grad():
+        gate.weight.copy_(torch.randn(I, K, generator=g) * 0.05)
+        up.weight.copy_(torch.randn(I, K, generator=g) * 0.05)
+    qg, qu = Int4Linear.from_linear(gate, 128).to(DEV), Int4Linear.from_linear(up, 128).to(DEV)
+    fused = Int4Linear.gate_up_pairs(qg, qu)
+    assert fused.fuses_norm
+    x = (torch.randn(M, K, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(dtype)
+    got = int4_linear(x.to(DEV), fused.qweight, fused.scales, fused.zeros, None, 128, silu_mul=True,
+                      norm_weight=w.to(DEV), norm_eps=1e-6)
+    torch.cuda.synchronize()
+    assert got.shape == (M, I)
+
+    xf = x.double().numpy()
+    rstd = 1.0 / np.sqrt((xf ** 2).mean(axis=1, keepdims=True) + 1e-6)
+    xn = _round(xf * rstd * w.double().numpy(), dtype)
+
+    def proj(q):
+        wq = dequantize_int4_ref(q.qweight.cpu().numpy(), q.scales.cpu().numpy(), q.zeros.cpu().numpy(), 128,
+                                 NAME[dtype])
+        ref = int4_linear_ref(xn, wq, None)
+        # The normalised operands may round one unit apart, which moves a
+        # projection by at most that unit times |w| summed over K.
+        return ref, 2 * RTOL[dtype] * np.abs(xn) @ np.abs(wq).T + RTOL[dtype] * np.abs(ref) + 1e-4
+
+    (gr, tg), (ur, tu) = proj(qg), proj(qu)
+    gv, uv = _round(gr, dtype), _round(ur, dtype)
+    act = _round(gv / (1.0 + np.exp(-gv)), dtype)
+    want = _round(act * uv, dtype)
+    # silu' is at most 1.1; the product carries both operands' bounds, then rounds.
+    tol = 1.1 * tg * np.abs(uv) + np.abs(act) * tu + tg * tu + 4 * RTOL[dtype] * np.abs(want) + 1e-4
+    err = np.abs(got.double().cpu().numpy() - want)
+    assert (err <= tol).all(), f"max err {err.max():.3e}"
+    # Normalising with torch first agrees within the same bound.
+    sep = int4_linear(F.rms_norm(x.to(DEV), (K,), w.to(DEV), 1e-6), fused.qweight, fused.scales, fused.zeros,
+                      None, 128, silu_mul=True)
+    torch.cuda.synchronize()
+    assert (np.abs(sep.double().cpu().numpy() - want) <= tol).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("N,K,gs", [(1152, 896, 128), (896, 4864, 128), (64, 256, 32)])
 def test_dequantize_is_bit_exact(dtype, N, K, gs):
     from nanoserve_amd.quant import int4_dequantize
