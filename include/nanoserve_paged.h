@@ -142,10 +142,12 @@ int ns_rope_reshape_and_cache(void* q_out, const void* query,
  *                         out [M, N/2] = round(round(silu(gate)) * up): the
  *                         SwiGLU of reference layers.py:108-109.
  * With norm_weight (a [K] `dtype` vector, 16-byte aligned) the rows of x are
- * first RMS-normalised in the same launch, round((x * rsqrt(mean(x^2) + eps))
- * * norm_weight), as torch's F.rms_norm computes the reference's RMSNorm
- * (layers.py:25-47) before q/k/v and gate/up; this needs K a multiple of 128
- * and at most 1024.
+ * RMS-normalised in the same launch, the reference's RMSNorm (layers.py:25-47)
+ * before q/k/v and gate/up: out = rsqrt(mean(x^2) + eps) * (round(x *
+ * norm_weight) · W^T) per row, then the bias and the epilogue.  The
+ * operands round at the precision of torch's F.rms_norm (round(x * rsqrt(..)
+ * * norm_weight) before the product); this needs K a multiple of 128 and at
+ * most 1024.
  * dtype is NS_DTYPE_F16 or NS_DTYPE_BF16.  N must be a multiple of 16, K and
  * group_size multiples of 32 with K a multiple of group_size; qweight 16-byte
  * aligned, out 8-byte aligned.  Up to 128 rows one kernel dequantises each
@@ -162,7 +164,7 @@ int ns_int4_linear(void* out, const void* x, int64_t x_stride_row,
  * ns_int4_linear_splitk -- ns_int4_linear with the K loop of long-K layers
  * split over several workgroups per output tile (down_proj of
  * Qwen2.5-0.5B: N = 896 is 56 tiles of 16 features, or 14 of 64, too few for
- * the device, each walking K = 4864).  Same operands, epilogues and prologue
+ * the device, each walking K = 4864).  Same operands, epilogues and RMSNorm
  * as ns_int4_linear; the fp32 partial sums of each split go to `workspace`
  * and the last split of a tile adds them in split order (deterministic) and
  * runs the epilogue.  The split count (up to 4) keeps tiles x splits within
@@ -198,7 +200,7 @@ int ns_int4_linear_splitk(void* out, const void* x, int64_t x_stride_row,
  * in that order, in the format of ns_int4_linear, with the rows of every
  * head in rotary-pair order: 16-row tile i of a head holds dims
  * [8i, 8i+8) then [head_dim/2 + 8i, +8).  With y = round(x · W^T + bias)
- * (and the RMSNorm prologue of ns_int4_linear when norm_weight is given),
+ * (and the RMSNorm of ns_int4_linear when norm_weight is given),
  * q and k are rotated exactly as ns_rope_reshape_and_cache rotates them;
  * q' goes to q_out ([M, num_heads, head_dim] contiguous, original dim
  * order), k' and v to slot_mapping's slots of k_cache / v_cache

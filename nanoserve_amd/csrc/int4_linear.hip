@@ -341,8 +341,8 @@ __global__ __launch_bounds__(WAVES * 64) void int4_linear_kernel(Int4LinearParam
     }
   }
 
-  // Whole 128-wide chunks, split between the waves.  The prologue has done
-  // them all when NORM is set.  Otherwise p.norm_weight is null, and testing
+  // Whole 128-wide chunks, split between the waves.  The NORM block above has
+  // done them all when NORM is set.  Otherwise p.norm_weight is null, and testing
   // it at run time keeps the compiler from deriving the chunk count and the
   // tail steps from K together: with `NORM ? 0 : p.K / 128` the 7-wave kernel
   // needed 74 VGPRs instead of 52 (two feature tiles: 128 instead of 77).
@@ -1193,7 +1193,7 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
   if (M == 0) return NS_OK;
   if (!out || !x || !qweight || !scales || !zeros) return NS_ERR_INVALID_ARG;
   if (epilogue == NS_EPILOGUE_RESIDUAL && (!residual || !aligned(residual, 8))) return NS_ERR_INVALID_ARG;
-  // The RMSNorm prologue needs every 128-wide chunk of K on its own wave.
+  // The fused RMSNorm needs every 128-wide chunk of K on its own wave.
   if (norm_weight && (K % 128 != 0 || K / 128 > 8)) return NS_ERR_UNSUPPORTED;
   if (norm_weight && !aligned(norm_weight, 16)) return NS_ERR_INVALID_ARG;
   // One MFMA row tile per 16 features; a K step of 32 lies inside one group.
@@ -1220,7 +1220,7 @@ int int4_linear_entry(void* out, const void* x, int64_t x_stride_row, const void
   p.K = K;
   p.group_size = group_size;
   p.groups = K / group_size;
-  // The GEMM has no RMSNorm prologue; its epilogue reads bias four at a time
+  // The GEMM does not fuse the RMSNorm; its epilogue reads bias four at a time
   // and its loads take whole 4-byte words of the zero-point table.
   // Its loads address x, the codes and the scales by 32-bit byte offsets.
   const int64_t esz = 2, lim = int64_t{1} << 32;
