@@ -333,12 +333,11 @@ __device__ __forceinline__ void decode_item(const AttnParams& p, uint32_t idx, u
 #pragma unroll
   for (int n = 0; n < NN; ++n) acc[n] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // Block id of the wave's tile `tile` >= 8 (BIG), from the table entries
-  // the wave loaded into `ids`.  Uniform, so the DMA addresses stay scalar.
-  // Tiles 0-7 come with the item and stay in scalar registers (ib): reading
-  // them back from LDS would put an LDS read and its wait in front of every
-  // chunk's loads, which measured 0.18 us per call slower on c1 (8.08 against
-  // 7.90) and 0.08 us on c2.
+  // Block id of the wave's tile `tile` >= CARRIED (BIG), from the table
+  // entries the wave loaded into `ids`.  Uniform, so the DMA addresses stay
+  // scalar.  The first CARRIED tiles' ids come with the item and stay in
+  // scalar registers (ib): reading them back from LDS would put an LDS read
+  // and its wait in front of those chunks' loads.
   const int64_t e_first = (wb + 16 * Cfg::CARRIED) >> bs_shift;  // table entry of the first tile not carried
   auto carried_block = [&](int tile) -> int64_t {
     int32_t v = ib.id[0];
