@@ -42,17 +42,33 @@ class RotaryEmbedding:
         emb = torch.cat((freqs, freqs), dim=-1)
         self.cos_cached = emb.cos().to(device)
         self.sin_cached = emb.sin().to(device)
+        self._stack_tables()
+
+    def _stack_tables(self) -> None:
+        # cos and sin side by side, [max_position, 2, head_dim], once per
+        # dtype: the float32 values rounded once, as the reference's per-step
+        # `.to(dtype)` rounds them, so one gather per forward pass yields both.
+        both = torch.stack((self.cos_cached, self.sin_cached), dim=1)
+        self._tables = {dt: both.to(dt) for dt in (torch.float16, torch.bfloat16)}
+        self._tables[torch.float32] = both
 
     def to(self, device) -> "RotaryEmbedding":
         self.cos_cached = self.cos_cached.to(device)
         self.sin_cached = self.sin_cached.to(device)
+        self._stack_tables()
         return self
 
     def cos_sin(self, positions: torch.Tensor, dtype: torch.dtype):
-        """Once per forward pass: cos, sin as [T, 1, head_dim] in `dtype` (layers.py:75-79)."""
-        cos = self.cos_cached.index_select(0, positions).unsqueeze(1).to(dtype)
-        sin = self.sin_cached.index_select(0, positions).unsqueeze(1).to(dtype)
-        return cos, sin
+        """Once per forward pass: cos, sin as [T, 1, head_dim] in `dtype` (layers.py:75-79).
+
+        Both are views of one gathered [T, 2, head_dim] tensor (row stride
+        2 * head_dim), the values of the reference's gather-then-convert."""
+        table = self._tables.get(dtype)
+        if table is None:
+            both = torch.stack((self.cos_cached, self.sin_cached), dim=1)
+            table = both.to(dtype)
+        cs = table.index_select(0, positions)
+        return cs[:, 0:1, :], cs[:, 1:2, :]
 
     @staticmethod
     def apply_and_cache(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
