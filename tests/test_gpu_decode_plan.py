@@ -9,7 +9,8 @@ against properties that do not restate how it is computed:
     batch) get no items, and each item's query row is the sequence's row;
   * item sizes never exceed the plan's tokens per item, which is a multiple of
     16 no smaller than the minimum, and the item count stays within the
-    buffer's capacity and the round target (or one item per pair);
+    buffer's capacity and the round target (or one item per pair, or, when
+    even the longest items leave more, the plan takes that longest length);
   * a plan of more items than the device has CUs lists its pairs longest
     sequence first (the items run in several rounds); a plan that runs in one
     round keeps the batch's order.
@@ -63,8 +64,11 @@ def _check(seq_lens, query_lens, hkv=2, d=64, bs=16, index_dtype=torch.int64):
     qsl = np.concatenate([[0], np.cumsum(query_lens)])
     decode_rows = [s for s, q in enumerate(query_lens) if q == 1]
     pairs = len(decode_rows) * hkv
-    # At most the round target (CUs x rounds, rounds <= 16) or one item per pair.
-    assert n <= max(256 * 16, pairs)
+    # At most the round target (CUs x rounds, rounds <= 16) or one item per pair,
+    # unless even the longest items (kMaxItemTokens = 4096, or the longest
+    # context below that) leave more: the plan then takes that length.
+    if n > max(256 * 16, pairs):
+        assert T == min(4096, -(-max(seq_lens) // 16) * 16), (n, T)
     seen = {}
     for idx, (s, qtok, t0, t1, first, nsplit, kvh, split) in enumerate(items):
         assert s in decode_rows and 0 <= kvh < hkv
@@ -156,6 +160,18 @@ def test_plan_of_a_mixed_batch_lists_only_decode_rows():
     qls = [1, 300, 1, 64, 1]
     _check(seqs, qls)
     _check([100, 200], [100, 200])  # no decode row at all: no items
+
+
+@pytest.mark.parametrize("num_seqs,max_len", [(64, 16384), (256, 16384), (512, 16384), (1024, 32768)])
+def test_plan_grid_slices_of_every_size(num_seqs, max_len):
+    # The plan kernel's grid writes the fewest whole passes of 8 items per
+    # workgroup that keep it within 256 workgroups: these batches' capacities
+    # (640, 2560, 5120, 18432 items) give slices of 8, 16, 24 and 32 items, the
+    # last on a grid of 576 workgroups.  Every slice must write its items whole.
+    rng = np.random.default_rng(num_seqs)
+    seqs = rng.integers(1, max_len, num_seqs, endpoint=True).tolist()
+    seqs[0] = max_len
+    _check(seqs, [1] * num_seqs)
 
 
 def test_plan_with_more_sequences_than_the_ranked_window():
